@@ -1,0 +1,149 @@
+/*
+ * sc_api.h -- C ABI of libsc, the MI355X (gfx950) implementation of the
+ * enumerate-and-sparse-coarsen SpMM/SpMV path of hosseinal/sparse-computation.
+ *
+ * Every entry point returns an int status (SC_OK == 0); on failure
+ * sc_last_error() returns a thread-local message.  No C++ exception crosses
+ * this boundary.  Objects are opaque and owned by the caller, who frees them
+ * with the matching *_free / *_destroy call.  Device pointers are plain
+ * `const float *` / `float *` allocated by the caller (hipMalloc, torch, ...);
+ * streams are passed as `void *` holding a hipStream_t (NULL = null stream).
+ *
+ * Each declaration names the reference interface it replaces (file:line in
+ * the reference tree).
+ */
+#ifndef SC_API_H
+#define SC_API_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SC_ABI_VERSION 1
+
+/* status codes */
+#define SC_OK 0
+#define SC_ERR_ARG 1         /* invalid argument */
+#define SC_ERR_IO 2          /* file cannot be opened / written */
+#define SC_ERR_FORMAT 3      /* malformed .mtx / .cfmtx / dictionary text */
+#define SC_ERR_HIP 4         /* HIP runtime error */
+#define SC_ERR_UNSUPPORTED 5 /* valid input outside what this build handles */
+#define SC_ERR_NOMEM 6       /* host allocation failed */
+#define SC_ERR_INTERNAL 7
+
+/* value kinds of a matrix (they decide how .cfmtx values are printed) */
+#define SC_VALUES_REAL 0
+#define SC_VALUES_INTEGER 1
+#define SC_VALUES_PATTERN 2
+
+/* .mtx reader modes */
+#define SC_MTX_SCIPY 0  /* scipy.io.mmread(p).tocsr(): duplicates summed   */
+#define SC_MTX_SYMLIB 1 /* sym_lib reader of the demos: duplicates kept     */
+
+typedef struct sc_csr sc_csr;     /* CSR matrix (host)                        */
+typedef struct sc_cfmtx sc_cfmtx; /* compressed format (host)                 */
+typedef struct sc_plan sc_plan;   /* compressed format resident on one GPU    */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *sc_last_error(void);
+int sc_abi_version(void);
+
+/* ---------------------------------------------------------------- patterns */
+
+/* build_patterns_map(kernel_m, kernel_n) / generate_pattern_dictionary(m, n)
+ * (code_gen/pattern_utiles/pattern_dictionary.py:29-46).  Writes the bit
+ * string of every id 0 .. 2^(km*kn)-2 into `bits` (km*kn chars + NUL each,
+ * stride km*kn+1); returns the count through *npat. */
+int sc_patterns(int32_t km, int32_t kn, char *bits, int64_t bits_len, int32_t *npat);
+
+/* ---------------------------------------------------------------- CSR / mtx */
+
+/* readCSRMatrixFromMTX (utils/Sparse_io.cpp:48-82) with mode SC_MTX_SYMLIB;
+ * scipy.io.mmread(path).tocsr() (code_gen/ss_format/format_generator.py:214-215)
+ * with mode SC_MTX_SCIPY. */
+int sc_mtx_read(const char *path, int32_t mode, sc_csr **out);
+/* Write a coordinate general .mtx (values as Python repr of the double). */
+int sc_mtx_write(const sc_csr *A, const char *path);
+/* Copy caller arrays into a new CSR (columns sorted and unique per row). */
+int sc_csr_create(int32_t m, int32_t n, const int32_t *indptr, const int32_t *indices,
+                  const double *data, int32_t value_kind, sc_csr **out);
+int sc_csr_info(const sc_csr *A, int32_t *m, int32_t *n, int64_t *nnz, int32_t *value_kind);
+/* Borrowed views, valid until sc_csr_free. */
+int sc_csr_arrays(const sc_csr *A, const int32_t **indptr, const int32_t **indices,
+                  const double **data);
+void sc_csr_free(sc_csr *A);
+
+/* ---------------------------------------------------------------- .cfmtx */
+
+/* csr_to_compressed_format_converter + transform_row_panel
+ * (code_gen/ss_format/format_generator.py:36-129).  km = row coarsen factor,
+ * kn = column pack (0 = 32 // pop).  dictionary_path NULL = enumerate all
+ * 2^km-1 patterns (format_generator.py:207-208); otherwise a
+ * --pattern_dictionary file (:200-205). */
+int sc_cfmtx_build(const sc_csr *A, int32_t km, int32_t kn, const char *dictionary_path,
+                   sc_cfmtx **out);
+/* format_writer (format_generator.py:132-160), byte-exact. */
+int sc_cfmtx_write(const sc_cfmtx *cf, const char *path);
+/* readCFMTXFile / readCompressedFormatMatrix (utils/Sparse_io.cpp:84-182, :243-250). */
+int sc_cfmtx_read(const char *path, sc_cfmtx **out);
+/* loadCfmtxMatrices (utils/Sparse_io.cpp:221-231, include/Sparse_io.h:17-24):
+ * the .cfmtx and its companion .mtx (sym_lib reader).  Path must end in .cfmtx. */
+int sc_load_cfmtx_matrices(const char *cfmtx_path, sc_csr **csr, sc_cfmtx **cf);
+/* readCSRMatrix (utils/Sparse_io.cpp:233-241): the companion .mtx only. */
+int sc_read_csr_matrix(const char *cfmtx_path, sc_csr **csr);
+/* companionMtxPathFromCFMTX (utils/Sparse_io.cpp:28-46). */
+int sc_companion_mtx_path(const char *cfmtx_path, char *buf, size_t buflen);
+
+/* Header of a .cfmtx: M, K, km, number of patterns, kn (as written), and
+ * the number of row panels ceil(M/km). */
+int sc_cfmtx_info(const sc_cfmtx *cf, int32_t *m, int32_t *n, int32_t *km, int32_t *npat,
+                  int32_t *kn, int32_t *npanels);
+/* Pattern i (data-block order): its bit string, printed id and pop, and
+ * borrowed views of RPP (npanels+1), CB and the fp32 values (what the
+ * reference's CompressedFormat<float> holds: CompressedFormat.h:88-107). */
+int sc_cfmtx_pattern(const sc_cfmtx *cf, int32_t i, const char **bits, int32_t *id, int32_t *pop,
+                     const int32_t **rpp, int64_t *nrpp, const int32_t **cb, int64_t *ncb,
+                     const float **vals, int64_t *nvals);
+/* Serialised text of a built .cfmtx (length through *len; buffer may be NULL
+ * to query the length). */
+int sc_cfmtx_text(const sc_cfmtx *cf, char *buf, int64_t buflen, int64_t *len);
+void sc_cfmtx_free(sc_cfmtx *cf);
+
+/* ---------------------------------------------------------------- GPU path */
+
+/* Plan flags */
+#define SC_PLAN_DROP_PADDING 1 /* omit the zero-valued padding slots on the device */
+
+/* allocateAndCopyMixedFormat (example_cuda/spmm_demo_gpu_utils.h:207-245) and
+ * the constructors of the generated classes SpMMMixePatternGeneralCacheLess /
+ * SpMVMixePatternDecomposeByRowSeperated: validate the format, flatten it
+ * into panel-major segments and upload it to the current HIP device.
+ * Every (panel, pattern) block of slots must use columns < K and hold
+ * pop values per slot; out-of-range formats are rejected here, so a kernel
+ * never reads outside the plan. */
+int sc_plan_create(const sc_cfmtx *cf, int32_t flags, sc_plan **out);
+/* Plan geometry: rows, cols, km, panels, device slots and values, segments. */
+int sc_plan_info(const sc_plan *plan, int32_t *m, int32_t *n, int32_t *km, int32_t *npanels,
+                 int64_t *nslots, int64_t *nvals, int64_t *nsegs);
+/* The pattern kernels: SpMMFullRowPanelGeneralKernel{km}With{kn}BlockCacheLess
+ * (example_cuda/spmm_demo_gpu_utils.h:1357-1664, large N) and
+ * SpmvComplexPatternDecomposeByRowSeperated (spmm_small_b_col_demo_gpu_utils.h
+ * :1061-2986 for small N, spmv_demo_gpu_utils.h:632-904 for N = 1).
+ * C = A*B with B row-major K x N and C row-major M x N, both on the plan's
+ * device.  C is overwritten (the reference accumulates into a pre-zeroed C;
+ * pass SC_ACCUMULATE for C += A*B).  waves_per_panel 0 = automatic. */
+#define SC_ACCUMULATE 1
+int sc_spmm(const sc_plan *plan, const float *dB, float *dC, int32_t N, int32_t flags,
+            int32_t waves_per_panel, void *hip_stream);
+/* y = A*x (N = 1). */
+int sc_spmv(const sc_plan *plan, const float *dx, float *dy, int32_t flags, void *hip_stream);
+void sc_plan_destroy(sc_plan *plan);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SC_API_H */

@@ -1,0 +1,152 @@
+"""Emit gfx950 HIP for the pattern kernels.
+
+One call produces one translation unit for a row coarsen factor ``km`` and a
+pattern dictionary:
+
+* one straight-line ``__device__`` body per pattern -- the panel rows of the
+  pattern are literal indices into the accumulator tile, the ``kn`` slots of a
+  pack are unrolled (``kn`` B-row loads, ``pop * kn`` value loads and
+  ``pop * kn`` FMA rows per step);
+* a dispatcher whose ``switch`` maps a segment's row mask to its body;
+* an ``extern "C"`` launcher ``sc_gen_<name>_launch`` and a parameter record
+  ``sc_gen_<name>_record`` (km, kn, waves, patterns, N variant, masks), so a
+  plan built for other parameters is rejected rather than mis-computed.
+
+The building blocks (lane mapping, B loads, wave64 reductions, the panel
+kernel) are hand-written in ``csrc/sc_kernels.hpp``; this module writes what
+the reference's generators write per pattern
+(code_gen/spmm/spmm_format_code_generator.py:74-223,
+code_gen/spmm_small_b_col/spmm_small_b_col_format_code_generator.py:4-323,
+code_gen/spmv/spmv_format_code_generator.py:4-213), for wave64 rather than
+warp32.
+"""
+from __future__ import annotations
+
+import re
+
+KINDS = ("spmm", "spmm_small_b_col", "spmv")
+
+
+def _rows(bits: str):
+    return [r for r, ch in enumerate(bits) if ch == "1"]
+
+
+def _mask(bits: str) -> int:
+    return sum(1 << r for r in _rows(bits))
+
+
+def body_name(bits: str) -> str:
+    return f"pattern_{bits}"
+
+
+def emit_body(km: int, bits: str, pid: int, kn: int, unroll: int) -> str:
+    rows = _rows(bits)
+    pop = len(rows)
+    out = []
+    out.append(f"// pattern id {pid}: bits {bits} -> panel rows {', '.join(map(str, rows))} "
+               f"(pop {pop}), packs of {kn} slot(s)")
+    out.append("template <int V>")
+    out.append(f"__device__ __forceinline__ void {body_name(bits)}(float (&acc)[{km}][V], "
+               "const sc::SegArgs &a) {")
+    if unroll > 1:
+        out.append(f"#pragma unroll {unroll}")
+    out.append(f"  for (int j = a.lo + a.s * {kn}; j < a.hi; j += a.S * {kn}) {{")
+    out.append(f"    const float *vp = a.vals + a.vb + (j - a.sb) * {pop};")
+    for q in range(kn):
+        out.append(f"    const int c{q} = a.cols[j + {q}];")
+    for q in range(kn):
+        out.append(f"    float b{q}[V];")
+        out.append(f"    sc::load_b<V>(b{q}, a, c{q});")
+    for q in range(kn):
+        for k in range(pop):
+            out.append(f"    const float v{q}_{k} = vp[{q * pop + k}];")
+    for q in range(kn):
+        for k, r in enumerate(rows):
+            out.append(f"    sc::fma_row<V>(acc[{r}], v{q}_{k}, b{q});")
+    out.append("  }")
+    out.append("}")
+    return "\n".join(out)
+
+
+def sanitize(name: str) -> str:
+    return re.sub(r"[^0-9A-Za-z_]", "_", name)
+
+
+def emit_unit(name: str, km: int, patterns, kn: int = 1, waves: int = 0, variant: int = 0,
+              unroll: int = 0, origin: str = "") -> str:
+    """Return the text of one generated translation unit.
+
+    ``patterns``: iterable of (bit string, id) in dictionary order.  Patterns
+    whose length differs from ``km`` or that have no ones never match a
+    panel (the format builder drops them) and get no body.
+    ``variant``: 0 = any N, otherwise the only N the launcher accepts.
+    """
+    if km < 1 or km > 20:
+        raise ValueError("km must be in 1..20")
+    if kn < 1:
+        raise ValueError("kernel_n (pack) must be >= 1 for generated kernels")
+    name = sanitize(name)
+    if unroll <= 0:
+        unroll = max(1, 4 // kn)
+    usable = []
+    seen = set()
+    for bits, pid in patterns:
+        if len(bits) != km or "1" not in bits or set(bits) - {"0", "1"}:
+            continue
+        if bits in seen:
+            continue
+        seen.add(bits)
+        usable.append((bits, int(pid)))
+    out = []
+    out.append("// Generated pattern kernels for gfx950 -- do not edit.")
+    if origin:
+        out.append(f"// {origin}")
+    out.append(f"// km={km} kn={kn} waves={waves} variant={variant} patterns={len(usable)}")
+    out.append('#include "sc_kernels.hpp"')
+    out.append("")
+    out.append(f"namespace sc_gen_{name} {{")
+    out.append("")
+    for bits, pid in usable:
+        out.append(emit_body(km, bits, pid, kn, unroll))
+        out.append("")
+    out.append("struct dispatch {")
+    out.append("  template <int KM, int V>")
+    out.append("  __device__ __forceinline__ static void run(int mask, float (&acc)[KM][V], "
+               "const sc::SegArgs &a) {")
+    out.append(f"    static_assert(KM == {km}, \"dispatcher generated for km={km}\");")
+    out.append("    switch (mask) {")
+    for bits, pid in usable:
+        out.append(f"      case {_mask(bits)}: {body_name(bits)}<V>(acc, a); break;  // id {pid}")
+    out.append("      default: break;")
+    out.append("    }")
+    out.append("  }")
+    out.append("};")
+    out.append("")
+    out.append(f"}}  // namespace sc_gen_{name}")
+    out.append("")
+    masks = ", ".join(f"{_mask(b)}u" for b, _ in usable) or "0u"
+    out.append(f'extern "C" __attribute__((visibility("default"))) const uint32_t '
+               f"sc_gen_{name}_masks[] = {{{masks}}};")
+    out.append(f'extern "C" __attribute__((visibility("default"))) const sc_gen_record '
+               f"sc_gen_{name}_record = {{{km}, {kn}, {waves}, {len(usable)}, {variant}, "
+               f"sc_gen_{name}_masks}};")
+    out.append("")
+    out.append(f'extern "C" __attribute__((visibility("default"))) hipError_t '
+               f"sc_gen_{name}_launch(const sc::DevView *v, const float *B, float *C, int N,")
+    out.append("                                         int accumulate, int waves, "
+               "hipStream_t stream) {")
+    if variant:
+        out.append(f"  if (N != {variant}) return hipErrorInvalidValue;")
+    if waves:
+        out.append(f"  if (waves <= 0) waves = {waves};")
+    out.append("  if (waves <= 0) waves = 1;")
+    out.append(f"  return sc::launch_panels<{km}, sc_gen_{name}::dispatch>(*v, B, C, N, accumulate, "
+               f"waves, {kn}, stream);")
+    out.append("}")
+    out.append("")
+    return "\n".join(out)
+
+
+def dictionary_patterns(ptd) -> list:
+    """(bits, id) pairs of a PatternTypeDictionary in insertion order."""
+    return [(bits, pid) for pid, bits in ptd.id_to_patten_bin.items()]

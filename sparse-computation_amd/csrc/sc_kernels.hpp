@@ -1,0 +1,253 @@
+// sc_kernels.hpp -- hand-written gfx950 building blocks of the pattern kernels.
+//
+// The code generators (code_gen/main_spmm.py, main_spmm_small_b_col.py,
+// main_spmv.py) emit one straight-line device function per enumerated
+// pattern and a `switch` over the pattern masks; this header supplies what
+// those functions are made of and the panel kernel that calls them.
+//
+// Execution model (wave64, CDNA4):
+//   * one workgroup owns one row panel of km rows, so every C row is written
+//     by exactly one workgroup -- no atomics, no pre-zeroed C (the reference
+//     launches one block per (panel, pattern) and atomically adds into a
+//     zeroed C: example_cuda/spmm_demo_gpu_utils.h:1357-1416);
+//   * the panel's slots (all its pattern segments, concatenated) are split
+//     between the W waves of the workgroup in pack-aligned ranges;
+//   * inside a wave, lanes are (slot sub-lane s, column group g): L lanes of a
+//     slot cover N columns with V floats each (V = 4, 2, 1 -> dwordx4/x2/x1
+//     loads of the B row), and S = 64 / L slots are in flight per step;
+//   * per lane the C tile is acc[KM][V] in VGPRs; a pattern body adds
+//     value(slot,row) * B[col(slot), c0 .. c0+V) into the rows of its mask
+//     only, with the row indices compile-time constants;
+//   * the S slot sub-lanes are reduced with a butterfly (ds_swizzle / DPP
+//     through __shfl_xor), then the W waves through LDS in a fixed order, so
+//     results are deterministic run to run.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sc {
+
+// Device view of a plan: the .cfmtx flattened panel-major.
+struct DevView {
+  const int4 *seg;        // per segment {rowmask, slot_begin, nslots, val_begin}
+  const int *panel_seg;   // [npanels + 1] segment range of each panel
+  const int *panel_slot;  // [npanels + 1] slot range of each panel
+  const int *cols;        // [nslots] B row (column of A) of every slot
+  const float *vals;      // [nvals] pop values per slot, ascending panel row
+  int M;                  // rows of A / C
+  int K;                  // columns of A / rows of B
+  int km;                 // rows per panel
+  int npanels;
+};
+
+// Everything a pattern body needs for one (segment, wave) range.
+struct SegArgs {
+  const int *__restrict__ cols;
+  const float *__restrict__ vals;
+  const float *__restrict__ Bc;  // B + c0 (first column of this lane's group)
+  int N;                         // columns of B and C
+  int lo, hi;                    // slot range [lo, hi) of this wave in the segment
+  int sb;                        // first slot of the segment
+  int vb;                        // first value of the segment
+  int s, S;                      // slot sub-lane and number of sub-lanes
+  bool cval;                     // this lane's column group lies inside N
+};
+
+template <int V>
+__device__ __forceinline__ void load_b(float (&b)[V], const SegArgs &a, int col) {
+  const float *p = a.Bc + (size_t)col * (size_t)a.N;
+  if constexpr (V == 4) {
+    float4 t = a.cval ? *reinterpret_cast<const float4 *>(p) : make_float4(0.f, 0.f, 0.f, 0.f);
+    b[0] = t.x;
+    b[1] = t.y;
+    b[2] = t.z;
+    b[3] = t.w;
+  } else if constexpr (V == 2) {
+    float2 t = a.cval ? *reinterpret_cast<const float2 *>(p) : make_float2(0.f, 0.f);
+    b[0] = t.x;
+    b[1] = t.y;
+  } else {
+    b[0] = a.cval ? *p : 0.f;
+  }
+}
+
+template <int V>
+__device__ __forceinline__ void fma_row(float (&acc)[V], float v, const float (&b)[V]) {
+#pragma unroll
+  for (int e = 0; e < V; ++e) acc[e] = __builtin_fmaf(v, b[e], acc[e]);
+}
+
+// Cross-lane sum over the S slot sub-lanes (lanes g, g+L, g+2L, ...).
+template <int KM, int V>
+__device__ __forceinline__ void reduce_slot_lanes(float (&acc)[KM][V], int L) {
+  for (int off = L; off < 64; off <<= 1) {
+#pragma unroll
+    for (int r = 0; r < KM; ++r)
+#pragma unroll
+      for (int e = 0; e < V; ++e) acc[r][e] += __shfl_xor(acc[r][e], off, 64);
+  }
+}
+
+template <int V>
+__device__ __forceinline__ void store_c(float *dst, const float (&v)[V], int accumulate) {
+  if constexpr (V == 4) {
+    float4 t = make_float4(v[0], v[1], v[2], v[3]);
+    if (accumulate) {
+      float4 o = *reinterpret_cast<const float4 *>(dst);
+      t.x += o.x;
+      t.y += o.y;
+      t.z += o.z;
+      t.w += o.w;
+    }
+    *reinterpret_cast<float4 *>(dst) = t;
+  } else if constexpr (V == 2) {
+    float2 t = make_float2(v[0], v[1]);
+    if (accumulate) {
+      float2 o = *reinterpret_cast<const float2 *>(dst);
+      t.x += o.x;
+      t.y += o.y;
+    }
+    *reinterpret_cast<float2 *>(dst) = t;
+  } else {
+    *dst = accumulate ? *dst + v[0] : v[0];
+  }
+}
+
+// The panel kernel.  D is the generated dispatcher: D::run<KM, V>(mask, acc,
+// args) runs the straight-line body of the pattern whose row mask is `mask`.
+// blockDim.x = 64 * W; dynamic LDS = W * KM * L * V floats when W > 1.
+template <int KM, int V, class D>
+__global__ void __launch_bounds__(1024) panel_kernel(DevView v, const float *__restrict__ B,
+                                                      float *__restrict__ C, int N, int L,
+                                                      int accumulate, int pack) {
+  extern __shared__ float red[];
+  const int panel = blockIdx.x;
+  const int W = blockDim.x >> 6;
+  const int w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int S = 64 / L;
+  const int g = lane & (L - 1);
+  const int s = lane / L;
+  const int p0 = v.panel_slot[panel];
+  const int p1 = v.panel_slot[panel + 1];
+  // pack-aligned share of the panel's slots for this wave
+  const int npk = (p1 - p0 + pack - 1) / pack;
+  const int per = ((npk + W - 1) / W) * pack;
+  const int a0 = p0 + w * per;
+  const int a1 = min(p1, a0 + per);
+  const int sg0 = v.panel_seg[panel];
+  const int sg1 = v.panel_seg[panel + 1];
+  const int row0 = panel * KM;
+  const int LV = L * V;
+  for (int cbase = 0; cbase < N; cbase += LV) {
+    const int c0 = cbase + g * V;
+    SegArgs args;
+    args.cols = v.cols;
+    args.vals = v.vals;
+    args.Bc = B + c0;
+    args.N = N;
+    args.s = s;
+    args.S = S;
+    args.cval = c0 < N;
+    float acc[KM][V];
+#pragma unroll
+    for (int r = 0; r < KM; ++r)
+#pragma unroll
+      for (int e = 0; e < V; ++e) acc[r][e] = 0.f;
+    for (int si = sg0; si < sg1; ++si) {
+      const int4 sd = v.seg[si];
+      const int lo = max(sd.y, a0);
+      const int hi = min(sd.y + sd.z, a1);
+      if (lo < hi) {
+        args.lo = lo;
+        args.hi = hi;
+        args.sb = sd.y;
+        args.vb = sd.w;
+        D::template run<KM, V>(sd.x, acc, args);
+      }
+    }
+    reduce_slot_lanes<KM, V>(acc, L);
+    if (W == 1) {
+      if (s == 0 && c0 < N) {
+#pragma unroll
+        for (int r = 0; r < KM; ++r)
+          if (row0 + r < v.M) store_c<V>(C + (size_t)(row0 + r) * N + c0, acc[r], accumulate);
+      }
+    } else {
+      if (s == 0) {
+#pragma unroll
+        for (int r = 0; r < KM; ++r)
+#pragma unroll
+          for (int e = 0; e < V; ++e) red[(w * KM + r) * LV + g * V + e] = acc[r][e];
+      }
+      __syncthreads();
+      for (int t = threadIdx.x; t < KM * LV; t += blockDim.x) {
+        const int r = t / LV;
+        const int c = t - r * LV;
+        float sum = 0.f;
+        for (int ww = 0; ww < W; ++ww) sum += red[(ww * KM + r) * LV + c];
+        const int row = row0 + r;
+        const int col = cbase + c;
+        if (row < v.M && col < N) {
+          float *dst = C + (size_t)row * N + col;
+          *dst = accumulate ? *dst + sum : sum;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Launch geometry for N columns: V floats per lane, L lanes per slot
+// (a power of two <= 64), LDS bytes for the cross-wave reduction.
+struct Geometry {
+  int V, L;
+  size_t lds;
+};
+
+inline Geometry geometry(int km, int N, int W) {
+  Geometry g;
+  g.V = (N % 4 == 0) ? 4 : (N % 2 == 0) ? 2 : 1;
+  const int groups = (N + g.V - 1) / g.V;
+  g.L = 1;
+  while (g.L < groups && g.L < 64) g.L <<= 1;
+  g.lds = W > 1 ? (size_t)W * km * g.L * g.V * sizeof(float) : 0;
+  return g;
+}
+
+template <int KM, class D>
+hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int accumulate, int W,
+                         int pack, hipStream_t stream) {
+  if (v.npanels <= 0 || N <= 0) return hipSuccess;
+  const Geometry g = geometry(KM, N, W);
+  dim3 grid((unsigned)v.npanels), block((unsigned)(64 * W));
+  switch (g.V) {
+    case 4:
+      hipLaunchKernelGGL((panel_kernel<KM, 4, D>), grid, block, g.lds, stream, v, B, C, N, g.L,
+                         accumulate, pack);
+      break;
+    case 2:
+      hipLaunchKernelGGL((panel_kernel<KM, 2, D>), grid, block, g.lds, stream, v, B, C, N, g.L,
+                         accumulate, pack);
+      break;
+    default:
+      hipLaunchKernelGGL((panel_kernel<KM, 1, D>), grid, block, g.lds, stream, v, B, C, N, g.L,
+                         accumulate, pack);
+      break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace sc
+
+// Record of the parameters a generated unit was produced with, so that a
+// runtime/codegen mismatch is an error instead of a silent wrong result.
+struct sc_gen_record {
+  int32_t km;         // rows per panel
+  int32_t kn;         // pack the bodies are unrolled for (segments must be multiples)
+  int32_t waves;      // waves per panel (0 = chosen at launch)
+  int32_t npatterns;  // number of pattern bodies
+  int32_t variant;    // 0 = any N, otherwise the only N accepted
+  const uint32_t *masks;  // row mask of every body (bit r = panel row r)
+};

@@ -1,0 +1,292 @@
+// sc_plan.hip -- device-resident plans and the GPU entry points of the C ABI.
+//
+// A plan is the .cfmtx flattened panel-major for one device:
+//   seg[]         {rowmask, slot_begin, nslots, val_begin} of every non-empty
+//                 (panel, pattern) segment, panels in order, patterns in
+//                 data-block order inside a panel;
+//   panel_seg[]   segment range of each panel;
+//   panel_slot[]  slot range of each panel;
+//   cols[]        int32 column (B row) of every slot;
+//   vals[]        fp32 values, pop per slot, ascending panel row.
+// The reference keeps P separate per-pattern arrays behind a device pointer
+// table and launches one block per (panel, pattern) pair
+// (example_cuda/spmm_demo_gpu_utils.h:38-67, 207-245); here one workgroup
+// reads one contiguous panel, and empty (panel, pattern) pairs cost nothing.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "sc_errors.hpp"
+#include "sc_format.hpp"
+#include "sc_kernels.hpp"
+
+const sc::Cfmtx &sc_cfmtx_ref(const sc_cfmtx *cf);
+
+// generated units (csrc/gen/sc_gen_builtin_km*.hip)
+#define SC_DECLARE_GEN(k)                                                                        \
+  extern "C" const sc_gen_record sc_gen_builtin_km##k##_record;                                  \
+  extern "C" hipError_t sc_gen_builtin_km##k##_launch(const sc::DevView *, const float *, float *, \
+                                                      int, int, int, hipStream_t);
+SC_DECLARE_GEN(1)
+SC_DECLARE_GEN(2)
+SC_DECLARE_GEN(3)
+SC_DECLARE_GEN(4)
+SC_DECLARE_GEN(5)
+SC_DECLARE_GEN(6)
+
+namespace {
+
+using LaunchFn = hipError_t (*)(const sc::DevView *, const float *, float *, int, int, int, hipStream_t);
+
+struct GenEntry {
+  const sc_gen_record *rec;
+  LaunchFn launch;
+};
+
+const GenEntry kBuiltin[] = {
+    {nullptr, nullptr},
+    {&sc_gen_builtin_km1_record, sc_gen_builtin_km1_launch},
+    {&sc_gen_builtin_km2_record, sc_gen_builtin_km2_launch},
+    {&sc_gen_builtin_km3_record, sc_gen_builtin_km3_launch},
+    {&sc_gen_builtin_km4_record, sc_gen_builtin_km4_launch},
+    {&sc_gen_builtin_km5_record, sc_gen_builtin_km5_launch},
+    {&sc_gen_builtin_km6_record, sc_gen_builtin_km6_launch},
+};
+constexpr int kMaxBuiltinKm = 6;
+
+void hip_check(hipError_t e, const char *what) {
+  if (e != hipSuccess) throw sc::Error{SC_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e)};
+}
+
+}  // namespace
+
+struct sc_plan {
+  int device = 0;
+  int32_t M = 0, K = 0, km = 0, npanels = 0;
+  int64_t nslots = 0, nvals = 0, nsegs = 0;
+  int32_t max_slots_per_panel = 0;
+  void *dmem = nullptr;  // one allocation holding every array
+  sc::DevView view{};
+  GenEntry gen{};
+};
+
+namespace {
+
+template <class T>
+size_t align_up(size_t off) {
+  return (off + 255) / 256 * 256;
+}
+
+sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
+  if (cf.km < 1) throw sc::Error{SC_ERR_FORMAT, "kernel_m must be >= 1"};
+  if (cf.km > kMaxBuiltinKm)
+    throw sc::Error{SC_ERR_UNSUPPORTED, "no pattern kernels built for kernel_m " + std::to_string(cf.km) +
+                                            " (1.." + std::to_string(kMaxBuiltinKm) + ")"};
+  const int32_t km = cf.km, M = cf.m, K = cf.n, npanels = cf.npanels();
+  const bool drop_pad = (flags & SC_PLAN_DROP_PADDING) != 0;
+  const GenEntry gen = kBuiltin[km];
+  std::vector<uint32_t> supported(gen.rec->masks, gen.rec->masks + gen.rec->npatterns);
+
+  // validate every pattern block against the header so no kernel can read
+  // outside the plan or write outside C
+  struct PatInfo {
+    uint32_t mask;
+    int pop;
+  };
+  std::vector<PatInfo> info(cf.patterns.size());
+  for (size_t i = 0; i < cf.patterns.size(); ++i) {
+    const sc::Pattern &p = cf.patterns[i];
+    uint32_t mask = 0;
+    int pop = 0;
+    for (size_t r = 0; r < p.bits.size(); ++r)
+      if (p.bits[r] == '1') {
+        if ((int)r >= km) throw sc::Error{SC_ERR_FORMAT, "pattern " + p.bits + " has a row outside the panel"};
+        mask |= 1u << r;
+        ++pop;
+      }
+    info[i] = {mask, pop};
+    if ((int64_t)p.rpp.size() < (int64_t)npanels + 1)
+      throw sc::Error{SC_ERR_FORMAT, "row-panel pointer shorter than ceil(rows/km)+1"};
+    if (p.rpp[0] < 0) throw sc::Error{SC_ERR_FORMAT, "negative row-panel pointer"};
+    for (int32_t q = 0; q < npanels; ++q)
+      if (p.rpp[(size_t)q + 1] < p.rpp[(size_t)q])
+        throw sc::Error{SC_ERR_FORMAT, "row-panel pointer is not monotone"};
+    const int64_t used = p.rpp[(size_t)npanels] - p.rpp[0];
+    if (used == 0) continue;
+    if (pop == 0) throw sc::Error{SC_ERR_FORMAT, "pattern with no rows holds slots"};
+    if ((int64_t)p.rpp[(size_t)npanels] > (int64_t)p.cb.size())
+      throw sc::Error{SC_ERR_FORMAT, "row-panel pointer runs past the column list"};
+    if ((int64_t)p.rpp[(size_t)npanels] * pop > (int64_t)p.val32.size())
+      throw sc::Error{SC_ERR_FORMAT, "fewer values than slots * pop"};
+    for (int64_t j = p.rpp[0]; j < p.rpp[(size_t)npanels]; ++j)
+      if (p.cb[(size_t)j] < 0 || p.cb[(size_t)j] >= K)
+        throw sc::Error{SC_ERR_FORMAT, "column index outside 0..cols-1"};
+    if (std::find(supported.begin(), supported.end(), mask) == supported.end())
+      throw sc::Error{SC_ERR_UNSUPPORTED, "no kernel body for pattern " + p.bits};
+  }
+
+  // flatten panel-major
+  std::vector<int4> seg;
+  std::vector<int32_t> panel_seg((size_t)npanels + 1), panel_slot((size_t)npanels + 1);
+  std::vector<int32_t> cols;
+  std::vector<float> vals;
+  int32_t max_pp = 0;
+  for (int32_t q = 0; q < npanels; ++q) {
+    panel_seg[(size_t)q] = (int32_t)seg.size();
+    panel_slot[(size_t)q] = (int32_t)cols.size();
+    for (size_t i = 0; i < cf.patterns.size(); ++i) {
+      const sc::Pattern &p = cf.patterns[i];
+      const int pop = info[i].pop;
+      int32_t a = p.rpp[(size_t)q], b = p.rpp[(size_t)q + 1];
+      if (b <= a) continue;
+      if (drop_pad) {
+        // trailing padding: repeated last column with all-zero values
+        while (b - 1 > a && p.cb[(size_t)b - 1] == p.cb[(size_t)b - 2]) {
+          bool zero = true;
+          for (int k = 0; k < pop; ++k)
+            if (p.val32[(size_t)(b - 1) * pop + k] != 0.0f || std::signbit(p.val32[(size_t)(b - 1) * pop + k]))
+              zero = false;
+          if (!zero) break;
+          --b;
+        }
+      }
+      if ((int64_t)cols.size() + (b - a) > INT32_MAX || (int64_t)vals.size() + (int64_t)(b - a) * pop > INT32_MAX)
+        throw sc::Error{SC_ERR_UNSUPPORTED, "plan larger than int32 offsets"};
+      seg.push_back(make_int4((int)info[i].mask, (int)cols.size(), b - a, (int)vals.size()));
+      cols.insert(cols.end(), p.cb.begin() + a, p.cb.begin() + b);
+      vals.insert(vals.end(), p.val32.begin() + (size_t)a * pop, p.val32.begin() + (size_t)b * pop);
+    }
+    max_pp = std::max(max_pp, (int32_t)cols.size() - panel_slot[(size_t)q]);
+  }
+  panel_seg[(size_t)npanels] = (int32_t)seg.size();
+  panel_slot[(size_t)npanels] = (int32_t)cols.size();
+
+  auto plan = std::make_unique<sc_plan>();
+  hip_check(hipGetDevice(&plan->device), "hipGetDevice");
+  plan->M = M;
+  plan->K = K;
+  plan->km = km;
+  plan->npanels = npanels;
+  plan->nslots = (int64_t)cols.size();
+  plan->nvals = (int64_t)vals.size();
+  plan->nsegs = (int64_t)seg.size();
+  plan->max_slots_per_panel = max_pp;
+  plan->gen = gen;
+
+  size_t off_seg = 0;
+  size_t off_pseg = align_up<int>(off_seg + seg.size() * sizeof(int4));
+  size_t off_pslot = align_up<int>(off_pseg + panel_seg.size() * sizeof(int32_t));
+  size_t off_cols = align_up<int>(off_pslot + panel_slot.size() * sizeof(int32_t));
+  size_t off_vals = align_up<int>(off_cols + cols.size() * sizeof(int32_t));
+  size_t total = align_up<int>(off_vals + vals.size() * sizeof(float));
+  hip_check(hipMalloc(&plan->dmem, total), "hipMalloc(plan)");
+  std::vector<unsigned char> host(total, 0);
+  std::memcpy(host.data() + off_seg, seg.data(), seg.size() * sizeof(int4));
+  std::memcpy(host.data() + off_pseg, panel_seg.data(), panel_seg.size() * sizeof(int32_t));
+  std::memcpy(host.data() + off_pslot, panel_slot.data(), panel_slot.size() * sizeof(int32_t));
+  std::memcpy(host.data() + off_cols, cols.data(), cols.size() * sizeof(int32_t));
+  std::memcpy(host.data() + off_vals, vals.data(), vals.size() * sizeof(float));
+  hipError_t e = hipMemcpy(plan->dmem, host.data(), total, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(plan->dmem);
+    hip_check(e, "hipMemcpy(plan)");
+  }
+  unsigned char *base = (unsigned char *)plan->dmem;
+  plan->view.seg = (const int4 *)(base + off_seg);
+  plan->view.panel_seg = (const int *)(base + off_pseg);
+  plan->view.panel_slot = (const int *)(base + off_pslot);
+  plan->view.cols = (const int *)(base + off_cols);
+  plan->view.vals = (const float *)(base + off_vals);
+  plan->view.M = M;
+  plan->view.K = K;
+  plan->view.km = km;
+  plan->view.npanels = npanels;
+  return plan.release();
+}
+
+// Waves per panel: enough waves in the grid to cover the 256 CUs several
+// times, but no wave with less than ~2 steps of S slots, and the LDS of the
+// cross-wave reduction within 64 KiB.
+int auto_waves(const sc_plan *p, int N) {
+  if (p->npanels == 0) return 1;
+  const sc::Geometry g1 = sc::geometry(p->km, N, 1);
+  const int S = 64 / g1.L;
+  const double avg = (double)p->nslots / p->npanels;
+  int w_occ = (int)std::max<int64_t>(1, 4096 / std::max(1, p->npanels));
+  int w_work = (int)std::max(1.0, avg / (2.0 * S));
+  int w = std::min(std::min(w_occ, w_work), 16);
+  while (w > 1 && sc::geometry(p->km, N, w).lds > 65536) --w;
+  return std::max(w, 1);
+}
+
+int launch(const sc_plan *p, const float *B, float *C, int32_t N, int32_t flags, int32_t waves,
+           void *stream) {
+  if (!p) throw sc::Error{SC_ERR_ARG, "null plan"};
+  if (N < 1) throw sc::Error{SC_ERR_ARG, "N must be >= 1"};
+  if (!B || !C) throw sc::Error{SC_ERR_ARG, "null device buffer"};
+  if (waves < 0 || waves > 16) throw sc::Error{SC_ERR_ARG, "waves per panel must be 0..16"};
+  int dev = -1;
+  hip_check(hipGetDevice(&dev), "hipGetDevice");
+  if (dev != p->device) throw sc::Error{SC_ERR_ARG, "plan lives on another device than the current one"};
+  if ((N % 4 == 0 && ((uintptr_t)B % 16 || (uintptr_t)C % 16)) ||
+      (N % 2 == 0 && ((uintptr_t)B % 8 || (uintptr_t)C % 8)) || (uintptr_t)B % 4 || (uintptr_t)C % 4)
+    throw sc::Error{SC_ERR_ARG, "B and C must be aligned to their vector width (16 B when N % 4 == 0)"};
+  int w = waves ? waves : auto_waves(p, N);
+  if (sc::geometry(p->km, N, w).lds > 65536) throw sc::Error{SC_ERR_ARG, "too many waves per panel for this N"};
+  hipError_t e = p->gen.launch(&p->view, B, C, N, (flags & SC_ACCUMULATE) ? 1 : 0, w, (hipStream_t)stream);
+  hip_check(e, "pattern kernel launch");
+  return SC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sc_plan_create(const sc_cfmtx *cf, int32_t flags, sc_plan **out) {
+  SC_GUARD([&] {
+    if (!cf || !out) throw sc::Error{SC_ERR_ARG, "null argument"};
+    if (flags & ~SC_PLAN_DROP_PADDING) throw sc::Error{SC_ERR_ARG, "unknown plan flags"};
+    *out = create_plan(sc_cfmtx_ref(cf), flags);
+  });
+}
+
+int sc_plan_info(const sc_plan *p, int32_t *m, int32_t *n, int32_t *km, int32_t *npanels, int64_t *nslots,
+                 int64_t *nvals, int64_t *nsegs) {
+  SC_GUARD([&] {
+    if (!p) throw sc::Error{SC_ERR_ARG, "null plan"};
+    if (m) *m = p->M;
+    if (n) *n = p->K;
+    if (km) *km = p->km;
+    if (npanels) *npanels = p->npanels;
+    if (nslots) *nslots = p->nslots;
+    if (nvals) *nvals = p->nvals;
+    if (nsegs) *nsegs = p->nsegs;
+  });
+}
+
+int sc_spmm(const sc_plan *plan, const float *dB, float *dC, int32_t N, int32_t flags,
+            int32_t waves_per_panel, void *hip_stream) {
+  SC_GUARD([&] {
+    if (flags & ~SC_ACCUMULATE) throw sc::Error{SC_ERR_ARG, "unknown flags"};
+    launch(plan, dB, dC, N, flags, waves_per_panel, hip_stream);
+  });
+}
+
+int sc_spmv(const sc_plan *plan, const float *dx, float *dy, int32_t flags, void *hip_stream) {
+  SC_GUARD([&] {
+    if (flags & ~SC_ACCUMULATE) throw sc::Error{SC_ERR_ARG, "unknown flags"};
+    launch(plan, dx, dy, 1, flags, 0, hip_stream);
+  });
+}
+
+void sc_plan_destroy(sc_plan *plan) {
+  if (!plan) return;
+  if (plan->dmem) (void)hipFree(plan->dmem);
+  delete plan;
+}
+
+}  // extern "C"

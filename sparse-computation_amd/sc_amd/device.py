@@ -1,0 +1,80 @@
+"""GPU side of the path: a plan (the .cfmtx resident on one device) and the
+pattern kernels, called through libsc's C ABI with torch tensors for the
+dense operands.  There is no CPU fallback: without a HIP device the calls
+raise."""
+from __future__ import annotations
+
+import ctypes as C
+
+from ._lib import check, lib, torch
+from .format import Cfmtx
+
+PLAN_DROP_PADDING = 1
+ACCUMULATE = 1
+
+
+def _stream_handle(stream):
+    if stream is None:
+        return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    if isinstance(stream, int):
+        return C.c_void_p(stream)
+    return C.c_void_p(stream.cuda_stream)
+
+
+class Plan:
+    """SpMMMixePatternGeneralCacheLess / SpMVMixePatternDecomposeByRowSeperated
+    of the reference (the generated classes of example_cuda/*_utils.h): the
+    format uploaded once, then launched on caller-owned B/C."""
+
+    def __init__(self, cf: Cfmtx, flags: int = 0):
+        h = C.c_void_p()
+        check(lib().sc_plan_create(cf._h, flags, C.byref(h)))
+        self._h = h
+
+    def __del__(self):
+        if getattr(self, "_h", None) and self._h.value:
+            lib().sc_plan_destroy(self._h)
+            self._h = C.c_void_p(None)
+
+    def info(self) -> dict:
+        v32 = [C.c_int32() for _ in range(4)]
+        v64 = [C.c_int64() for _ in range(3)]
+        check(lib().sc_plan_info(self._h, *[C.byref(x) for x in v32], *[C.byref(x) for x in v64]))
+        return dict(zip(("m", "n", "km", "npanels", "nslots", "nvals", "nsegs"),
+                        [x.value for x in v32 + v64]))
+
+    @staticmethod
+    def _check_operand(t, rows, cols, name):
+        if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous float32 tensor on the GPU")
+        if t.numel() != rows * cols:
+            raise ValueError(f"{name} must hold {rows}x{cols} elements, got {tuple(t.shape)}")
+
+    def spmm(self, B, C_out=None, accumulate=False, waves=0, stream=None):
+        """C = A @ B (B: K x N row-major float32 CUDA tensor)."""
+        info = self.info()
+        N = B.shape[1] if B.dim() == 2 else 1
+        self._check_operand(B, info["n"], N, "B")
+        if C_out is None:
+            C_out = torch.empty((info["m"], N), dtype=torch.float32, device=B.device)
+        self._check_operand(C_out, info["m"], N, "C")
+        check(lib().sc_spmm(self._h, C.c_void_p(B.data_ptr()), C.c_void_p(C_out.data_ptr()), N,
+                            ACCUMULATE if accumulate else 0, waves, _stream_handle(stream)))
+        return C_out
+
+    def spmm_ptr(self, b_ptr: int, c_ptr: int, N: int, flags: int = 0, waves: int = 0,
+                 stream=None) -> None:
+        """Raw-pointer form (no shape checks): for timing loops."""
+        check(lib().sc_spmm(self._h, C.c_void_p(b_ptr), C.c_void_p(c_ptr), N, flags, waves,
+                            _stream_handle(stream)))
+
+    def spmv(self, x, y=None, accumulate=False, stream=None):
+        """y = A @ x (x: length-K float32 CUDA tensor)."""
+        info = self.info()
+        self._check_operand(x, info["n"], 1, "x")
+        if y is None:
+            y = torch.empty(info["m"], dtype=torch.float32, device=x.device)
+        self._check_operand(y, info["m"], 1, "y")
+        check(lib().sc_spmv(self._h, C.c_void_p(x.data_ptr()), C.c_void_p(y.data_ptr()),
+                            ACCUMULATE if accumulate else 0, _stream_handle(stream)))
+        return y

@@ -1,0 +1,167 @@
+"""GPU parity: the pattern kernels (through libsc's C ABI) against the CPU
+oracle on the same seeded inputs.
+
+Floating point: max relative error <= 1e-5 normalised by (|A| |B|)_ij
+against the fp64 product of the same fp32 operands.
+Integer-valued inputs (the reference's all-ones fixture matrix times a
+small-integer B): every partial sum is exact in fp32, so the GPU result must
+equal the oracle's spmm_csr_float / spmv_csr_float restatement bit for bit.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+import sc_amd
+from cases import REL_TOL, csr_f32, oracle_check, synth_case
+from conftest import FIXTURE_STEM, REF_MATRICES
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def run_spmm(A, B, km, kn, flags=0, waves=0, accumulate=None):
+    cf = sc_amd.Cfmtx.build(A, km, kn)
+    plan = sc_amd.Plan(cf, flags)
+    Bt = torch.from_numpy(np.ascontiguousarray(B, np.float32)).to(DEV)
+    if accumulate is not None:
+        Ct = torch.from_numpy(accumulate.copy()).to(DEV)
+        plan.spmm(Bt, Ct, accumulate=True, waves=waves)
+    else:
+        Ct = torch.full((A.shape[0], B.shape[1]), float("nan"), device=DEV)  # must be overwritten
+        plan.spmm(Bt, Ct, waves=waves)
+    torch.cuda.synchronize()
+    return Ct.cpu().numpy()
+
+
+@pytest.mark.parametrize("n", [1, 2, 4, 32, 64, 128])
+@pytest.mark.parametrize("km", [1, 2, 3, 4, 5, 6])
+def test_spmm_512_uniform(km, n):
+    A, B = synth_case(512, 512, 0.10, n, seed=0x5EED0000 + 2000 + km * 10 + n)
+    C = run_spmm(A, B, km, 1)
+    err, _ = oracle_check(A, B, C)
+    assert err <= REL_TOL, (km, n, err)
+
+
+@pytest.mark.parametrize("kn", [2, 3, 5, 8, 0])
+def test_spmm_column_packs(kn):
+    A, B = synth_case(512, 512, 0.20, 32, seed=0x5EED0000 + 1000 + kn)
+    C = run_spmm(A, B, 4, kn)
+    err, _ = oracle_check(A, B, C)
+    assert err <= REL_TOL, (kn, err)
+
+
+@pytest.mark.parametrize("n", [3, 5, 33, 100, 256, 300, 512])
+def test_spmm_odd_and_wide_n(n):
+    A, B = synth_case(96, 160, 0.15, n, seed=0x5EED0000 + 7000 + n)
+    C = run_spmm(A, B, 4, 1)
+    err, _ = oracle_check(A, B, C)
+    assert err <= REL_TOL, (n, err)
+
+
+@pytest.mark.parametrize("waves", [1, 2, 3, 8, 16])
+def test_spmm_waves_per_panel(waves):
+    A, B = synth_case(256, 384, 0.25, 64, seed=0x5EED0000 + 8000 + waves)
+    C = run_spmm(A, B, 4, 2, waves=waves)
+    err, _ = oracle_check(A, B, C)
+    assert err <= REL_TOL, (waves, err)
+
+
+def test_spmm_ragged_rows_and_empty_rows():
+    # 37 rows (not a multiple of km), rows 5..12 and the last row empty
+    rng = np.random.default_rng(5)
+    dense = (rng.random((37, 53)) < 0.3) * rng.standard_normal((37, 53))
+    dense[5:13] = 0
+    dense[-1] = 0
+    ip = np.concatenate([[0], np.cumsum((dense != 0).sum(1))]).astype(np.int32)
+    ix = np.nonzero(dense)[1].astype(np.int32)
+    dx = dense[dense != 0].astype(np.float32).astype(np.float64)
+    A = sc_amd.Csr.from_arrays(37, 53, ip, ix, dx)
+    B = sc_amd.synth_dense(53 * 8, 77).reshape(53, 8)
+    for km in (1, 3, 4, 5, 6):
+        C = run_spmm(A, B, km, 2)
+        err, _ = oracle_check(A, B, C)
+        assert err <= REL_TOL, (km, err)
+        assert np.all(C[5:13] == 0) and np.all(C[-1] == 0)
+
+
+def test_spmm_empty_matrix_overwrites_c():
+    A = sc_amd.Csr.from_arrays(10, 12, np.zeros(11, np.int32), [], [])
+    B = sc_amd.synth_dense(12 * 4, 3).reshape(12, 4)
+    C = run_spmm(A, B, 4, 1)
+    assert np.all(C == 0)
+
+
+def test_spmm_accumulate_flag():
+    A, B = synth_case(128, 128, 0.2, 32, seed=11)
+    C0 = sc_amd.synth_dense(128 * 32, 12).reshape(128, 32)
+    C = run_spmm(A, B, 4, 1, accumulate=C0)
+    ip, ix, ax = csr_f32(A)
+    c64, cab = O.spmm_f64(128, 32, ip, ix, ax, B)
+    err = O.max_rel_err(C - C0.astype(np.float64), c64, cab + np.abs(C0))
+    assert err <= REL_TOL
+
+
+def test_spmm_drop_padding_plan():
+    # Dropping the zero padding moves the slot split between waves, so the
+    # fp32 summation order (not the exact sum) changes: both must pass the
+    # tolerance, and the plan must hold fewer slots.
+    A, B = synth_case(512, 512, 0.2, 64, seed=21)
+    cf = sc_amd.Cfmtx.build(A, 4, 8)
+    assert sc_amd.Plan(cf, sc_amd.PLAN_DROP_PADDING).info()["nslots"] < sc_amd.Plan(cf).info()["nslots"]
+    C1 = run_spmm(A, B, 4, 8)
+    C2 = run_spmm(A, B, 4, 8, flags=sc_amd.PLAN_DROP_PADDING)
+    assert oracle_check(A, B, C1)[0] <= REL_TOL
+    assert oracle_check(A, B, C2)[0] <= REL_TOL
+
+
+@pytest.mark.parametrize("n", [1, 32, 128])
+def test_spmm_structured_4096(n):
+    A, B = synth_case(4096, 4096, 0.10, n, seed=0x5EED0000 + 4000 + n, structured=True)
+    C = run_spmm(A, B, 4, 1)
+    err, _ = oracle_check(A, B, C)
+    assert err <= REL_TOL, (n, err)
+
+
+@pytest.mark.parametrize("km,kn", [(4, 2), (4, 3), (2, 5), (6, 8), (1, 2), (3, 1)])
+def test_fixture_matrix_bit_exact(km, kn):
+    """The reference's own matrix (values 1) times integer B: exact sums."""
+    mtx = os.path.join(REF_MATRICES, FIXTURE_STEM + ".mtx")
+    if os.path.exists(mtx):
+        A = sc_amd.Csr.from_mtx(mtx)
+    else:  # the GPU box has no reference tree: same shape/density, values 1
+        A0 = sc_amd.Csr.synth_uniform(512, 512, 0.4, 1.0, 99)
+        ip, ix, _ = A0.arrays()
+        A = sc_amd.Csr.from_arrays(512, 512, ip, ix, np.ones(len(ix)))
+    rng = np.random.default_rng(km * 10 + kn)
+    for n in (1, 4, 64):
+        B = rng.integers(-3, 4, size=(512, n)).astype(np.float32)
+        C = run_spmm(A, B, km, kn)
+        ip, ix, ax = csr_f32(A)
+        ref = O.spmm_csr_float(512, n, ip, ix, ax, B)
+        assert np.array_equal(C, ref), (km, kn, n)
+
+
+def test_spmv_matches_reference_cpu_path():
+    A, B = synth_case(512, 512, 0.30, 1, seed=0x5EED0000 + 0)
+    cf = sc_amd.Cfmtx.build(A, 1, 1)
+    plan = sc_amd.Plan(cf)
+    x = torch.from_numpy(B[:, 0].copy()).to(DEV)
+    y = plan.spmv(x)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    err, _ = oracle_check(A, B, y.reshape(-1, 1))
+    assert err <= REL_TOL
+    ip, ix, ax = csr_f32(A)
+    ycpu = O.spmv_csr_float(512, ip, ix, ax, B[:, 0])
+    assert np.max(np.abs(y - ycpu)) <= 1e-5 * max(1.0, float(np.abs(ycpu).max()))
+
+
+def test_plan_rejects_bad_device_buffer_shapes():
+    A, B = synth_case(64, 64, 0.2, 4, seed=1)
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1))
+    with pytest.raises(ValueError):
+        plan.spmm(torch.zeros((63, 4), device=DEV))
