@@ -142,6 +142,34 @@ int sc_spmm(const sc_plan *plan, const float *dB, float *dC, int32_t N, int32_t 
 int sc_spmv(const sc_plan *plan, const float *dx, float *dy, int32_t flags, void *hip_stream);
 void sc_plan_destroy(sc_plan *plan);
 
+/* ------------------------------------------------------- generated kernels */
+
+/* Parameters a generated kernel unit was emitted with by code_gen/main_spmm.py,
+ * main_spmm_small_b_col.py or main_spmv.py (exported as sc_gen_<name>_record).
+ * The reference bakes the same parameters into its generated headers
+ * (code_gen/spmm/spmm_format_code_generator.py:7-223) but never checks them
+ * against the loaded matrix. */
+typedef struct sc_gen_record {
+  int32_t km;             /* rows per panel                                    */
+  int32_t kn;             /* slots per unrolled pack (segments must be multiples) */
+  int32_t waves;          /* waves per panel, 0 = chosen at launch             */
+  int32_t npatterns;      /* number of pattern bodies                          */
+  int32_t variant;        /* 0 = any N, otherwise the only N accepted          */
+  const uint32_t *masks;  /* row mask of each body (bit r = panel row r)       */
+} sc_gen_record;
+
+/* sc_gen_<name>_launch of a generated unit. */
+typedef int (*sc_gen_launch_fn)(const void *view, const float *B, float *C, int N, int accumulate,
+                                int waves, void *hip_stream);
+
+/* Launch a generated unit on a plan after checking that the unit fits it:
+ * same km, a pack that divides every segment, a body for every pattern the
+ * plan holds and, for fixed-N units, the same N.  Replaces the launch in the
+ * generated classes' execute() (spmm_demo_gpu_utils.h:1700-1720). */
+int sc_spmm_generated(const sc_plan *plan, const sc_gen_record *rec, sc_gen_launch_fn launch,
+                      const float *dB, float *dC, int32_t N, int32_t flags,
+                      int32_t waves_per_panel, void *hip_stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -165,16 +165,18 @@ def build(M, K, indptr, indices, data, km, kn, patterns: dict):
     return out
 
 
-def _value_text(v: float, pad: bool, is_int: bool) -> str:
+def _value_text(v: float, pad: bool) -> str:
+    # format_generator.py:80-81 vstacks a float64 csr_matrix of padding rows
+    # onto the input, which upcasts integer and pattern fields to float64:
+    # every real value prints as a float (an integer field's 7 as "7.0").
     if pad:
         return "0"
-    if is_int:
-        return str(int(v))
     return repr(float(v))
 
 
 def cfmtx_text(cf: dict, patterns: dict, is_int: bool = False) -> str:
-    """format_writer (format_generator.py:132-160) as a string."""
+    """format_writer (format_generator.py:132-160) as a string.  `is_int` is
+    accepted for the field kind of the .mtx but does not change the text."""
     out = [f"{cf['num_row']} {cf['num_col']} {cf['kernel_rows']} {len(patterns)} "
            f"{cf['vector_length']}\n"]
     for key, val in patterns.items():
@@ -182,7 +184,7 @@ def cfmtx_text(cf: dict, patterns: dict, is_int: bool = False) -> str:
     for i in range(len(patterns)):
         out.append(" ".join(str(x) for x in cf["rpp"][i]) + "\n")
         out.append(" ".join(str(int(x)) for x in cf["cb"][i]) + "\n")
-        out.append(" ".join(_value_text(v, p, is_int)
+        out.append(" ".join(_value_text(v, p)
                             for v, p in zip(cf["vals"][i].tolist(), cf["pad"][i].tolist())) + "\n")
     return "".join(out)
 

@@ -68,6 +68,49 @@ def emit_body(km: int, bits: str, pid: int, kn: int, unroll: int) -> str:
     return "\n".join(out)
 
 
+def wide_name(bits: str) -> str:
+    return f"wide_{bits}"
+
+
+def _wide_step(rows, pop, slots, indent):
+    """Straight-line code for `slots` consecutive slots starting at j."""
+    out = [f"{indent}const float *vp = a.vals + a.vb + (j - a.sb) * {pop};"]
+    for q in range(slots):
+        out.append(f"{indent}const int c{q} = a.cols[j + {q}];")
+    for q in range(slots):
+        out.append(f"{indent}float b{q}[V];")
+        out.append(f"{indent}sc::load_row<V>(b{q}, a, c{q});")
+    for q in range(slots):
+        for k in range(pop):
+            out.append(f"{indent}const float v{q}_{k} = vp[{q * pop + k}];")
+    for q in range(slots):
+        for k, r in enumerate(rows):
+            out.append(f"{indent}sc::fma_row<V>(acc[{r}], v{q}_{k}, b{q});")
+    return out
+
+
+def emit_wide_body(km: int, bits: str, pid: int, kn: int, unroll_slots: int = 8) -> str:
+    """Wide-path body: the whole wave shares each slot; `unroll_slots`
+    (a multiple of kn) B-row loads in flight, then kn-slot packs for the tail."""
+    rows = _rows(bits)
+    pop = len(rows)
+    U = kn * max(1, -(-unroll_slots // kn))
+    out = [f"// pattern id {pid}: bits {bits} -> panel rows {', '.join(map(str, rows))} "
+           f"(pop {pop}); wave-wide slots, {U} per step",
+           "template <int V>",
+           f"__device__ __forceinline__ void {wide_name(bits)}(float (&acc)[{km}][V], "
+           "const sc::WideArgs &a) {",
+           "  int j = a.lo;",
+           f"  for (; j + {U} <= a.hi; j += {U}) {{"]
+    out += _wide_step(rows, pop, U, "    ")
+    out.append("  }")
+    out.append(f"  for (; j < a.hi; j += {kn}) {{")
+    out += _wide_step(rows, pop, kn, "    ")
+    out.append("  }")
+    out.append("}")
+    return "\n".join(out)
+
+
 def sanitize(name: str) -> str:
     return re.sub(r"[^0-9A-Za-z_]", "_", name)
 
@@ -109,7 +152,18 @@ def emit_unit(name: str, km: int, patterns, kn: int = 1, waves: int = 0, variant
     for bits, pid in usable:
         out.append(emit_body(km, bits, pid, kn, unroll))
         out.append("")
+        out.append(emit_wide_body(km, bits, pid, kn))
+        out.append("")
     out.append("struct dispatch {")
+    out.append("  template <int KM, int V>")
+    out.append("  __device__ __forceinline__ static void run_wide(int mask, float (&acc)[KM][V], "
+               "const sc::WideArgs &a) {")
+    out.append("    switch (mask) {")
+    for bits, pid in usable:
+        out.append(f"      case {_mask(bits)}: {wide_name(bits)}<V>(acc, a); break;  // id {pid}")
+    out.append("      default: break;")
+    out.append("    }")
+    out.append("  }")
     out.append("  template <int KM, int V>")
     out.append("  __device__ __forceinline__ static void run(int mask, float (&acc)[KM][V], "
                "const sc::SegArgs &a) {")

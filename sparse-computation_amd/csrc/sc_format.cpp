@@ -516,10 +516,10 @@ std::string cfmtx_text(const Cfmtx &cf) {
       if (cf.has_exact && pt.pad[j]) {
         s.push_back('0');
       } else if (cf.has_exact) {
-        if (cf.kind == VALUES_INTEGER)
-          append_int(s, (int64_t)pt.val64[j]);
-        else
-          s += py_repr(pt.val64[j]);
+        // integer and pattern fields print as floats too: the reference
+        // stacks its float64 padding rows onto the CSR first
+        // (format_generator.py:80-81), which upcasts the values
+        s += py_repr(pt.val64[j]);
       } else {
         s += py_repr((double)pt.val32[j]);
       }

@@ -26,6 +26,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "sc_api.h"
+
 namespace sc {
 
 // Device view of a plan: the .cfmtx flattened panel-major.
@@ -33,12 +35,15 @@ struct DevView {
   const int4 *seg;        // per segment {rowmask, slot_begin, nslots, val_begin}
   const int *panel_seg;   // [npanels + 1] segment range of each panel
   const int *panel_slot;  // [npanels + 1] slot range of each panel
+  const int *panel_val;   // [npanels + 1] value range of each panel
   const int *cols;        // [nslots] B row (column of A) of every slot
   const float *vals;      // [nvals] pop values per slot, ascending panel row
   int M;                  // rows of A / C
   int K;                  // columns of A / rows of B
   int km;                 // rows per panel
   int npanels;
+  int max_pslots;         // most slots in one panel
+  int max_pvals;          // most values in one panel
 };
 
 // Everything a pattern body needs for one (segment, wave) range.
@@ -199,15 +204,198 @@ __global__ void __launch_bounds__(1024) panel_kernel(DevView v, const float *__r
   }
 }
 
+// ---------------------------------------------------------------------------
+// Wide path (N a multiple of 64): the whole wave works on one slot at a time,
+// lane l owning columns cbase + l*V .. + V-1.  Column indices and values are
+// then wave-uniform: they come through the scalar cache (s_load), the B-row
+// address is formed on the SALU, and the VALU only runs the FMAs.  Bodies
+// unroll UW slots so UW B-row loads are in flight per wave.
+// ---------------------------------------------------------------------------
+constexpr int UW = 8;
+
+struct WideArgs {
+  const int *__restrict__ cols;
+  const float *__restrict__ vals;
+  const char *__restrict__ Bc;  // B + cbase (wave-uniform)
+  unsigned lane_off;            // lane * V * 4 bytes
+  unsigned row_bytes;           // N * 4
+  int N;
+  int lo, hi;  // slot range of this wave in the segment
+  int sb, vb;  // first slot / first value of the segment
+};
+
+// 32-bit byte offsets from a uniform base (K * N * 4 < 2^32 is checked at
+// launch): the load becomes global_load saddr + voffset.
+template <int V>
+__device__ __forceinline__ void load_row(float (&b)[V], const WideArgs &a, int col) {
+  const float *p = reinterpret_cast<const float *>(a.Bc + ((unsigned)col * a.row_bytes + a.lane_off));
+  if constexpr (V == 4) {
+    const float4 t = *reinterpret_cast<const float4 *>(p);
+    b[0] = t.x;
+    b[1] = t.y;
+    b[2] = t.z;
+    b[3] = t.w;
+  } else if constexpr (V == 2) {
+    const float2 t = *reinterpret_cast<const float2 *>(p);
+    b[0] = t.x;
+    b[1] = t.y;
+  } else {
+    b[0] = *p;
+  }
+}
+
+// One workgroup per row panel, W waves splitting its slots.  With STAGE the
+// workgroup first copies the panel's column indices and values (contiguous in
+// the plan) into LDS with coalesced loads, so the slot loop reads them at LDS
+// latency instead of waiting on a cache miss per batch; the staging area is
+// reused for the cross-wave reduction afterwards.
+template <int KM, int V, bool STAGE, class D>
+__global__ void __launch_bounds__(1024)
+    wide_kernel(const int4 *__restrict__ seg, const int *__restrict__ panel_seg,
+                const int *__restrict__ panel_slot, const int *__restrict__ panel_val,
+                const int *__restrict__ cols, const float *__restrict__ vals,
+                const float *__restrict__ B, float *__restrict__ C, int M, int N, int accumulate,
+                int pack, int stage_cols) {
+  extern __shared__ float smem[];
+  const int panel = blockIdx.x;
+  const int W = blockDim.x >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int p0 = panel_slot[panel];
+  const int p1 = panel_slot[panel + 1];
+  const int npk = (p1 - p0 + pack - 1) / pack;
+  const int per = ((npk + W - 1) / W) * pack;
+  const int a0 = p0 + w * per;
+  const int a1 = min(p1, a0 + per);
+  const int sg0 = panel_seg[panel];
+  const int sg1 = panel_seg[panel + 1];
+  const int row0 = panel * KM;
+  constexpr int CW = 64 * V;  // columns per chunk
+
+  const int *cs = cols;
+  const float *vs = vals;
+  if constexpr (STAGE) {
+    const int q0 = panel_val[panel];
+    const int q1 = panel_val[panel + 1];
+    int *lc = reinterpret_cast<int *>(smem);
+    float *lv = smem + stage_cols;
+    for (int t = threadIdx.x; t < p1 - p0; t += blockDim.x) lc[t] = cols[p0 + t];
+    for (int t = threadIdx.x; t < q1 - q0; t += blockDim.x) lv[t] = vals[q0 + t];
+    __syncthreads();
+    cs = lc - p0;  // indexed with global slot numbers
+    vs = lv - q0;
+  }
+
+  for (int cbase = 0; cbase < N; cbase += CW) {
+    WideArgs args;
+    args.cols = cs;
+    args.vals = vs;
+    args.Bc = reinterpret_cast<const char *>(B + cbase);
+    args.lane_off = (unsigned)(lane * V * sizeof(float));
+    args.row_bytes = (unsigned)(N * sizeof(float));
+    args.N = N;
+    float acc[KM][V];
+#pragma unroll
+    for (int r = 0; r < KM; ++r)
+#pragma unroll
+      for (int e = 0; e < V; ++e) acc[r][e] = 0.f;
+    for (int si = sg0; si < sg1; ++si) {
+      const int4 sd = seg[si];
+      const int lo = max(sd.y, a0);
+      const int hi = min(sd.y + sd.z, a1);
+      if (lo < hi) {
+        args.lo = lo;
+        args.hi = hi;
+        args.sb = sd.y;
+        args.vb = sd.w;
+        D::template run_wide<KM, V>(sd.x, acc, args);
+      }
+    }
+    const int c0 = cbase + lane * V;
+    if (W == 1) {
+#pragma unroll
+      for (int r = 0; r < KM; ++r)
+        if (row0 + r < M) store_c<V>(C + (size_t)(row0 + r) * N + c0, acc[r], accumulate);
+    } else {
+      float *red = smem;
+      if constexpr (STAGE) __syncthreads();  // every wave is done with the staged stream
+#pragma unroll
+      for (int r = 0; r < KM; ++r)
+#pragma unroll
+        for (int e = 0; e < V; ++e) red[(w * KM + r) * CW + lane * V + e] = acc[r][e];
+      __syncthreads();
+      for (int t = threadIdx.x; t < KM * CW; t += blockDim.x) {
+        const int r = t / CW;
+        const int c = t - r * CW;
+        float sum = 0.f;
+        for (int ww = 0; ww < W; ++ww) sum += red[(ww * KM + r) * CW + c];
+        const int row = row0 + r;
+        if (row < M) {
+          float *dst = C + (size_t)row * N + cbase + c;
+          *dst = accumulate ? *dst + sum : sum;
+        }
+      }
+      __syncthreads();
+    }
+    if constexpr (STAGE) {
+      if (cbase + CW < N) {  // restage: the reduction overwrote the stream
+        const int q0 = panel_val[panel];
+        const int q1 = panel_val[panel + 1];
+        int *lc = reinterpret_cast<int *>(smem);
+        float *lv = smem + stage_cols;
+        for (int t = threadIdx.x; t < p1 - p0; t += blockDim.x) lc[t] = cols[p0 + t];
+        for (int t = threadIdx.x; t < q1 - q0; t += blockDim.x) lv[t] = vals[q0 + t];
+        __syncthreads();
+      }
+    }
+  }
+}
+
+// Floats per lane of the wide path for N columns, 0 if N does not fit it.
+inline int wide_v(int N, long long K = 0) {
+  if ((long long)K * N * 4 >= (1LL << 32)) return 0;
+  if (N % 256 == 0) return 4;
+  if (N == 128) return 2;
+  if (N == 64) return 1;
+  return 0;
+}
+
 // Launch geometry for N columns: V floats per lane, L lanes per slot
 // (a power of two <= 64), LDS bytes for the cross-wave reduction.
 struct Geometry {
   int V, L;
+  bool wide;
+  bool stage;         // wide path stages the panel stream in LDS
+  int stage_cols;     // floats reserved for column indices in LDS
   size_t lds;
 };
 
-inline Geometry geometry(int km, int N, int W) {
+constexpr size_t kStageLimit = 64 * 1024;
+
+inline Geometry geometry(int km, int N, int W, long long K = 0, int max_pslots = -1,
+                         int max_pvals = -1) {
   Geometry g;
+  g.stage = false;
+  g.stage_cols = 0;
+  const int wv = wide_v(N, K);
+  if (wv) {
+    g.wide = true;
+    g.V = wv;
+    g.L = 64;
+    const size_t red = W > 1 ? (size_t)W * km * 64 * wv * sizeof(float) : 0;
+    g.lds = red;
+    if (max_pslots >= 0) {
+      const int sc = (max_pslots + 3) / 4 * 4;
+      const size_t st = ((size_t)sc + (size_t)max_pvals) * 4;
+      if (st <= kStageLimit) {
+        g.stage = true;
+        g.stage_cols = sc;
+        g.lds = st > red ? st : red;
+      }
+    }
+    return g;
+  }
+  g.wide = false;
   g.V = (N % 4 == 0) ? 4 : (N % 2 == 0) ? 2 : 1;
   const int groups = (N + g.V - 1) / g.V;
   g.L = 1;
@@ -220,8 +408,25 @@ template <int KM, class D>
 hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int accumulate, int W,
                          int pack, hipStream_t stream) {
   if (v.npanels <= 0 || N <= 0) return hipSuccess;
-  const Geometry g = geometry(KM, N, W);
+  const Geometry g = geometry(KM, N, W, v.K, v.max_pslots, v.max_pvals);
   dim3 grid((unsigned)v.npanels), block((unsigned)(64 * W));
+  if (g.wide) {
+#define SC_WIDE(VV, ST)                                                                           \
+  hipLaunchKernelGGL((wide_kernel<KM, VV, ST, D>), grid, block, g.lds, stream, v.seg, v.panel_seg, \
+                     v.panel_slot, v.panel_val, v.cols, v.vals, B, C, v.M, N, accumulate, pack,    \
+                     g.stage_cols)
+    if (g.stage) {
+      if (g.V == 4) SC_WIDE(4, true);
+      else if (g.V == 2) SC_WIDE(2, true);
+      else SC_WIDE(1, true);
+    } else {
+      if (g.V == 4) SC_WIDE(4, false);
+      else if (g.V == 2) SC_WIDE(2, false);
+      else SC_WIDE(1, false);
+    }
+#undef SC_WIDE
+    return hipGetLastError();
+  }
   switch (g.V) {
     case 4:
       hipLaunchKernelGGL((panel_kernel<KM, 4, D>), grid, block, g.lds, stream, v, B, C, N, g.L,
@@ -240,14 +445,3 @@ hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int 
 }
 
 }  // namespace sc
-
-// Record of the parameters a generated unit was produced with, so that a
-// runtime/codegen mismatch is an error instead of a silent wrong result.
-struct sc_gen_record {
-  int32_t km;         // rows per panel
-  int32_t kn;         // pack the bodies are unrolled for (segments must be multiples)
-  int32_t waves;      // waves per panel (0 = chosen at launch)
-  int32_t npatterns;  // number of pattern bodies
-  int32_t variant;    // 0 = any N, otherwise the only N accepted
-  const uint32_t *masks;  // row mask of every body (bit r = panel row r)
-};

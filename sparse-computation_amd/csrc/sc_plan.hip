@@ -69,6 +69,9 @@ struct sc_plan {
   int32_t M = 0, K = 0, km = 0, npanels = 0;
   int64_t nslots = 0, nvals = 0, nsegs = 0;
   int32_t max_slots_per_panel = 0;
+  int32_t kn = 0;            // column pack of the .cfmtx header
+  bool dropped_pad = false;  // padding slots omitted on the device
+  std::vector<uint32_t> masks;  // row masks of the patterns holding slots
   void *dmem = nullptr;  // one allocation holding every array
   sc::DevView view{};
   GenEntry gen{};
@@ -132,12 +135,15 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   // flatten panel-major
   std::vector<int4> seg;
   std::vector<int32_t> panel_seg((size_t)npanels + 1), panel_slot((size_t)npanels + 1);
+  std::vector<int32_t> panel_val((size_t)npanels + 1);
+  int32_t max_pv = 0;
   std::vector<int32_t> cols;
   std::vector<float> vals;
   int32_t max_pp = 0;
   for (int32_t q = 0; q < npanels; ++q) {
     panel_seg[(size_t)q] = (int32_t)seg.size();
     panel_slot[(size_t)q] = (int32_t)cols.size();
+    panel_val[(size_t)q] = (int32_t)vals.size();
     for (size_t i = 0; i < cf.patterns.size(); ++i) {
       const sc::Pattern &p = cf.patterns[i];
       const int pop = info[i].pop;
@@ -161,9 +167,11 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
       vals.insert(vals.end(), p.val32.begin() + (size_t)a * pop, p.val32.begin() + (size_t)b * pop);
     }
     max_pp = std::max(max_pp, (int32_t)cols.size() - panel_slot[(size_t)q]);
+    max_pv = std::max(max_pv, (int32_t)vals.size() - panel_val[(size_t)q]);
   }
   panel_seg[(size_t)npanels] = (int32_t)seg.size();
   panel_slot[(size_t)npanels] = (int32_t)cols.size();
+  panel_val[(size_t)npanels] = (int32_t)vals.size();
 
   auto plan = std::make_unique<sc_plan>();
   hip_check(hipGetDevice(&plan->device), "hipGetDevice");
@@ -176,11 +184,20 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   plan->nsegs = (int64_t)seg.size();
   plan->max_slots_per_panel = max_pp;
   plan->gen = gen;
+  plan->kn = cf.kn;
+  plan->dropped_pad = drop_pad;
+  for (size_t i = 0; i < cf.patterns.size(); ++i) {
+    const sc::Pattern &p = cf.patterns[i];
+    if (p.rpp[(size_t)npanels] > p.rpp[0] &&
+        std::find(plan->masks.begin(), plan->masks.end(), info[i].mask) == plan->masks.end())
+      plan->masks.push_back(info[i].mask);
+  }
 
   size_t off_seg = 0;
   size_t off_pseg = align_up<int>(off_seg + seg.size() * sizeof(int4));
   size_t off_pslot = align_up<int>(off_pseg + panel_seg.size() * sizeof(int32_t));
-  size_t off_cols = align_up<int>(off_pslot + panel_slot.size() * sizeof(int32_t));
+  size_t off_pval = align_up<int>(off_pslot + panel_slot.size() * sizeof(int32_t));
+  size_t off_cols = align_up<int>(off_pval + panel_val.size() * sizeof(int32_t));
   size_t off_vals = align_up<int>(off_cols + cols.size() * sizeof(int32_t));
   size_t total = align_up<int>(off_vals + vals.size() * sizeof(float));
   hip_check(hipMalloc(&plan->dmem, total), "hipMalloc(plan)");
@@ -188,6 +205,7 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   std::memcpy(host.data() + off_seg, seg.data(), seg.size() * sizeof(int4));
   std::memcpy(host.data() + off_pseg, panel_seg.data(), panel_seg.size() * sizeof(int32_t));
   std::memcpy(host.data() + off_pslot, panel_slot.data(), panel_slot.size() * sizeof(int32_t));
+  std::memcpy(host.data() + off_pval, panel_val.data(), panel_val.size() * sizeof(int32_t));
   std::memcpy(host.data() + off_cols, cols.data(), cols.size() * sizeof(int32_t));
   std::memcpy(host.data() + off_vals, vals.data(), vals.size() * sizeof(float));
   hipError_t e = hipMemcpy(plan->dmem, host.data(), total, hipMemcpyHostToDevice);
@@ -199,12 +217,15 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   plan->view.seg = (const int4 *)(base + off_seg);
   plan->view.panel_seg = (const int *)(base + off_pseg);
   plan->view.panel_slot = (const int *)(base + off_pslot);
+  plan->view.panel_val = (const int *)(base + off_pval);
   plan->view.cols = (const int *)(base + off_cols);
   plan->view.vals = (const float *)(base + off_vals);
   plan->view.M = M;
   plan->view.K = K;
   plan->view.km = km;
   plan->view.npanels = npanels;
+  plan->view.max_pslots = max_pp;
+  plan->view.max_pvals = max_pv;
   return plan.release();
 }
 
@@ -213,32 +234,59 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
 // cross-wave reduction within 64 KiB.
 int auto_waves(const sc_plan *p, int N) {
   if (p->npanels == 0) return 1;
-  const sc::Geometry g1 = sc::geometry(p->km, N, 1);
+  const sc::Geometry g1 = sc::geometry(p->km, N, 1, p->K, p->view.max_pslots, p->view.max_pvals);
   const int S = 64 / g1.L;
   const double avg = (double)p->nslots / p->npanels;
   int w_occ = (int)std::max<int64_t>(1, 4096 / std::max(1, p->npanels));
   int w_work = (int)std::max(1.0, avg / (2.0 * S));
   int w = std::min(std::min(w_occ, w_work), 16);
-  while (w > 1 && sc::geometry(p->km, N, w).lds > 65536) --w;
+  while (w > 1 && sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals).lds > 65536) --w;
   return std::max(w, 1);
 }
 
-int launch(const sc_plan *p, const float *B, float *C, int32_t N, int32_t flags, int32_t waves,
-           void *stream) {
+// Does a generated unit fit this plan?  (km, pack, pattern bodies, N)
+void check_record(const sc_plan *p, const sc_gen_record *rec, int32_t N) {
+  if (!rec) throw sc::Error{SC_ERR_ARG, "null generated-kernel record"};
+  if (rec->km != p->km)
+    throw sc::Error{SC_ERR_ARG, "kernels generated for km=" + std::to_string(rec->km) + ", plan has km=" +
+                                    std::to_string(p->km)};
+  if (rec->kn > 1) {
+    if (p->dropped_pad)
+      throw sc::Error{SC_ERR_ARG, "kernels unrolled for packs of " + std::to_string(rec->kn) +
+                                      " need the padded plan (no SC_PLAN_DROP_PADDING)"};
+    if (p->kn <= 0 || p->kn % rec->kn != 0)
+      throw sc::Error{SC_ERR_ARG, "kernels unrolled for packs of " + std::to_string(rec->kn) +
+                                      " do not divide the .cfmtx kernel_n " + std::to_string(p->kn)};
+  }
+  if (rec->variant != 0 && rec->variant != N)
+    throw sc::Error{SC_ERR_ARG, "kernels generated for N=" + std::to_string(rec->variant) + ", called with N=" +
+                                    std::to_string(N)};
+  for (uint32_t m : p->masks) {
+    bool found = false;
+    for (int32_t i = 0; i < rec->npatterns && !found; ++i) found = rec->masks[i] == m;
+    if (!found) throw sc::Error{SC_ERR_UNSUPPORTED, "generated kernels have no body for row mask " + std::to_string(m)};
+  }
+}
+
+int launch(const sc_plan *p, const sc_gen_record *rec, sc_gen_launch_fn fn, const float *B, float *C,
+           int32_t N, int32_t flags, int32_t waves, void *stream) {
   if (!p) throw sc::Error{SC_ERR_ARG, "null plan"};
+  if (!fn) throw sc::Error{SC_ERR_ARG, "null generated-kernel launcher"};
   if (N < 1) throw sc::Error{SC_ERR_ARG, "N must be >= 1"};
   if (!B || !C) throw sc::Error{SC_ERR_ARG, "null device buffer"};
   if (waves < 0 || waves > 16) throw sc::Error{SC_ERR_ARG, "waves per panel must be 0..16"};
+  check_record(p, rec, N);
   int dev = -1;
   hip_check(hipGetDevice(&dev), "hipGetDevice");
   if (dev != p->device) throw sc::Error{SC_ERR_ARG, "plan lives on another device than the current one"};
   if ((N % 4 == 0 && ((uintptr_t)B % 16 || (uintptr_t)C % 16)) ||
       (N % 2 == 0 && ((uintptr_t)B % 8 || (uintptr_t)C % 8)) || (uintptr_t)B % 4 || (uintptr_t)C % 4)
     throw sc::Error{SC_ERR_ARG, "B and C must be aligned to their vector width (16 B when N % 4 == 0)"};
-  int w = waves ? waves : auto_waves(p, N);
-  if (sc::geometry(p->km, N, w).lds > 65536) throw sc::Error{SC_ERR_ARG, "too many waves per panel for this N"};
-  hipError_t e = p->gen.launch(&p->view, B, C, N, (flags & SC_ACCUMULATE) ? 1 : 0, w, (hipStream_t)stream);
-  hip_check(e, "pattern kernel launch");
+  int w = waves ? waves : (rec->waves ? rec->waves : auto_waves(p, N));
+  if (sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals).lds > 65536)
+    throw sc::Error{SC_ERR_ARG, "too many waves per panel for this N"};
+  int e = fn(&p->view, B, C, N, (flags & SC_ACCUMULATE) ? 1 : 0, w, stream);
+  hip_check((hipError_t)e, "pattern kernel launch");
   return SC_OK;
 }
 
@@ -272,14 +320,24 @@ int sc_spmm(const sc_plan *plan, const float *dB, float *dC, int32_t N, int32_t 
             int32_t waves_per_panel, void *hip_stream) {
   SC_GUARD([&] {
     if (flags & ~SC_ACCUMULATE) throw sc::Error{SC_ERR_ARG, "unknown flags"};
-    launch(plan, dB, dC, N, flags, waves_per_panel, hip_stream);
+    if (!plan) throw sc::Error{SC_ERR_ARG, "null plan"};
+    launch(plan, plan->gen.rec, (sc_gen_launch_fn)plan->gen.launch, dB, dC, N, flags, waves_per_panel, hip_stream);
+  });
+}
+
+int sc_spmm_generated(const sc_plan *plan, const sc_gen_record *rec, sc_gen_launch_fn fn, const float *dB,
+                      float *dC, int32_t N, int32_t flags, int32_t waves_per_panel, void *hip_stream) {
+  SC_GUARD([&] {
+    if (flags & ~SC_ACCUMULATE) throw sc::Error{SC_ERR_ARG, "unknown flags"};
+    launch(plan, rec, fn, dB, dC, N, flags, waves_per_panel, hip_stream);
   });
 }
 
 int sc_spmv(const sc_plan *plan, const float *dx, float *dy, int32_t flags, void *hip_stream) {
   SC_GUARD([&] {
     if (flags & ~SC_ACCUMULATE) throw sc::Error{SC_ERR_ARG, "unknown flags"};
-    launch(plan, dx, dy, 1, flags, 0, hip_stream);
+    if (!plan) throw sc::Error{SC_ERR_ARG, "null plan"};
+    launch(plan, plan->gen.rec, (sc_gen_launch_fn)plan->gen.launch, dx, dy, 1, flags, 0, hip_stream);
   });
 }
 

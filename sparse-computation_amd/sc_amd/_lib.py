@@ -52,6 +52,7 @@ _SIGS = {
     "sc_spmm": ([vp, vp, vp, i32, i32, i32, vp], C.c_int),
     "sc_spmv": ([vp, vp, vp, i32, vp], C.c_int),
     "sc_plan_destroy": ([vp], None),
+    "sc_spmm_generated": ([vp, vp, vp, vp, vp, i32, i32, i32, vp], C.c_int),
     "sc_synth_uniform": ([i32, i32, C.c_double, C.c_double, u64, C.POINTER(vp)], C.c_int),
     "sc_synth_blocks": ([i32, i32, C.c_double, C.c_double, u64, C.POINTER(vp)], C.c_int),
     "sc_synth_dense": ([f32p, i64, u64], C.c_int),

@@ -21,6 +21,24 @@ def _stream_handle(stream):
     return C.c_void_p(stream.cuda_stream)
 
 
+class GeneratedUnit:
+    """A kernel unit emitted by code_gen/main_spmm.py, main_spmm_small_b_col.py
+    or main_spmv.py and compiled to a shared object: its record (km, kn,
+    masks, N variant) and launcher, looked up as sc_gen_<name>_record /
+    sc_gen_<name>_launch."""
+
+    def __init__(self, so_path: str, name: str):
+        self.lib = C.CDLL(so_path)
+        self.name = name
+        self.record = C.c_void_p.in_dll(self.lib, f"sc_gen_{name}_record")
+        self.record_ptr = C.cast(C.addressof(self.record), C.c_void_p)
+        self.launch = C.cast(getattr(self.lib, f"sc_gen_{name}_launch"), C.c_void_p)
+
+    def info(self) -> dict:
+        f = (C.c_int32 * 5).from_address(C.addressof(self.record))
+        return dict(zip(("km", "kn", "waves", "npatterns", "variant"), list(f)))
+
+
 class Plan:
     """SpMMMixePatternGeneralCacheLess / SpMVMixePatternDecomposeByRowSeperated
     of the reference (the generated classes of example_cuda/*_utils.h): the
@@ -67,6 +85,21 @@ class Plan:
         """Raw-pointer form (no shape checks): for timing loops."""
         check(lib().sc_spmm(self._h, C.c_void_p(b_ptr), C.c_void_p(c_ptr), N, flags, waves,
                             _stream_handle(stream)))
+
+    def spmm_generated(self, unit: GeneratedUnit, B, C_out=None, accumulate=False, waves=0,
+                       stream=None):
+        """C = A @ B through a generated kernel unit (checked against the plan)."""
+        info = self.info()
+        N = B.shape[1] if B.dim() == 2 else 1
+        self._check_operand(B, info["n"], N, "B")
+        if C_out is None:
+            C_out = torch.empty((info["m"], N), dtype=torch.float32, device=B.device)
+        self._check_operand(C_out, info["m"], N, "C")
+        check(lib().sc_spmm_generated(self._h, unit.record_ptr, unit.launch,
+                                      C.c_void_p(B.data_ptr()), C.c_void_p(C_out.data_ptr()), N,
+                                      ACCUMULATE if accumulate else 0, waves,
+                                      _stream_handle(stream)))
+        return C_out
 
     def spmv(self, x, y=None, accumulate=False, stream=None):
         """y = A @ x (x: length-K float32 CUDA tensor)."""

@@ -5,6 +5,7 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 for p in (ROOT, os.path.join(ROOT, "sparse-computation_amd"), os.path.join(ROOT, "oracle"),
+          os.path.join(ROOT, "sparse-computation_amd", "code_gen"),
           os.path.join(ROOT, "tests")):
     if p not in sys.path:
         sys.path.insert(0, p)

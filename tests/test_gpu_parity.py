@@ -165,3 +165,12 @@ def test_plan_rejects_bad_device_buffer_shapes():
     plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1))
     with pytest.raises(ValueError):
         plan.spmm(torch.zeros((63, 4), device=DEV))
+
+
+def test_spmm_wide_unstaged_dense_panels():
+    # panels of km=6 rows over 4096 dense-ish columns hold more than 64 KiB of
+    # stream, so the wide kernel reads columns/values from global memory
+    A, B = synth_case(12, 4096, 0.9, 128, seed=31)
+    C = run_spmm(A, B, 6, 1)
+    err, _ = oracle_check(A, B, C)
+    assert err <= REL_TOL, err
