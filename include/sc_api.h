@@ -116,6 +116,7 @@ void sc_cfmtx_free(sc_cfmtx *cf);
 
 /* Plan flags */
 #define SC_PLAN_DROP_PADDING 1 /* omit the zero-valued padding slots on the device */
+#define SC_PLAN_TILED 2        /* also build the split-K LDS-tiled copy (opt-in)    */
 
 /* allocateAndCopyMixedFormat (example_cuda/spmm_demo_gpu_utils.h:207-245) and
  * the constructors of the generated classes SpMMMixePatternGeneralCacheLess /

@@ -72,14 +72,14 @@ def wide_name(bits: str) -> str:
     return f"wide_{bits}"
 
 
-def _wide_step(rows, pop, slots, indent):
+def _wide_step(rows, pop, slots, indent, loader="sc::load_row"):
     """Straight-line code for `slots` consecutive slots starting at j."""
     out = [f"{indent}const float *vp = a.vals + a.vb + (j - a.sb) * {pop};"]
     for q in range(slots):
         out.append(f"{indent}const int c{q} = a.cols[j + {q}];")
     for q in range(slots):
         out.append(f"{indent}float b{q}[V];")
-        out.append(f"{indent}sc::load_row<V>(b{q}, a, c{q});")
+        out.append(f"{indent}{loader}<V>(b{q}, a, c{q});")
     for q in range(slots):
         for k in range(pop):
             out.append(f"{indent}const float v{q}_{k} = vp[{q * pop + k}];")
@@ -106,6 +106,42 @@ def emit_wide_body(km: int, bits: str, pid: int, kn: int, unroll_slots: int = 8)
     out.append("  }")
     out.append(f"  for (; j < a.hi; j += {kn}) {{")
     out += _wide_step(rows, pop, kn, "    ")
+    out.append("  }")
+    out.append("}")
+    return "\n".join(out)
+
+
+def tile_name(bits: str) -> str:
+    return f"tile_{bits}"
+
+
+def emit_tile_body(km: int, bits: str, pid: int, unroll_slots: int = 8) -> str:
+    """Tiled-path body: wave-wide slots of one K block, B rows read from the
+    LDS tile.  Sub-segments are short (a segment split over K blocks), so every
+    step is a full batch of `unroll_slots`: slots past the end re-read the
+    last slot's column and contribute a zero value."""
+    rows = _rows(bits)
+    pop = len(rows)
+    U = unroll_slots
+    out = [f"// pattern id {pid}: bits {bits} -> panel rows {', '.join(map(str, rows))} "
+           f"(pop {pop}); B rows from the LDS tile, {U} per step",
+           "template <int V>",
+           f"__device__ __forceinline__ void {tile_name(bits)}(float (&acc)[{km}][V], "
+           "const sc::TileArgs &a) {",
+           f"  for (int j = a.lo; j < a.hi; j += {U}) {{",
+           "    const int last = a.hi - 1 - j;  // last valid offset in this batch",
+           f"    const float *vp = a.vals + a.vb + (j - a.sb) * {pop};"]
+    for q in range(U):
+        out.append(f"    const int c{q} = a.cols[j + min({q}, last)];")
+    for q in range(U):
+        out.append(f"    float b{q}[V];")
+        out.append(f"    sc::load_tile<V>(b{q}, a, c{q});")
+    for q in range(U):
+        for k in range(pop):
+            out.append(f"    const float v{q}_{k} = {q} <= last ? vp[{q * pop + k}] : 0.0f;")
+    for q in range(U):
+        for k, r in enumerate(rows):
+            out.append(f"    sc::fma_row<V>(acc[{r}], v{q}_{k}, b{q});")
     out.append("  }")
     out.append("}")
     return "\n".join(out)
@@ -154,7 +190,18 @@ def emit_unit(name: str, km: int, patterns, kn: int = 1, waves: int = 0, variant
         out.append("")
         out.append(emit_wide_body(km, bits, pid, kn))
         out.append("")
+        out.append(emit_tile_body(km, bits, pid))
+        out.append("")
     out.append("struct dispatch {")
+    out.append("  template <int KM, int V>")
+    out.append("  __device__ __forceinline__ static void run_tile(int mask, float (&acc)[KM][V], "
+               "const sc::TileArgs &a) {")
+    out.append("    switch (mask) {")
+    for bits, pid in usable:
+        out.append(f"      case {_mask(bits)}: {tile_name(bits)}<V>(acc, a); break;  // id {pid}")
+    out.append("      default: break;")
+    out.append("    }")
+    out.append("  }")
     out.append("  template <int KM, int V>")
     out.append("  __device__ __forceinline__ static void run_wide(int mask, float (&acc)[KM][V], "
                "const sc::WideArgs &a) {")

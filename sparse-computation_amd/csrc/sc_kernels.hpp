@@ -26,6 +26,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "sc_api.h"
 
 namespace sc {
@@ -44,6 +46,27 @@ struct DevView {
   int npanels;
   int max_pslots;         // most slots in one panel
   int max_pvals;          // most values in one panel
+  // K-block-major copy of the stream for the tiled kernel (null if the plan
+  // has too little B reuse for it): for K block kb and panel p the
+  // sub-segments (the part of each segment whose columns fall in the block)
+  // are tseg[kp_seg[kb*(npanels+1)+p] .. kp_seg[kb*(npanels+1)+p+1]), their
+  // slots and values contiguous in tcols / tvals.
+  const int4 *tseg;       // {rowmask, slot_begin, nslots, val_begin} in tcols/tvals
+  const int *kp_seg;      // [nkb * (npanels + 1)]
+  const int *kp_slot;     // [nkb * (npanels + 1)] first tcols slot of (kb, panel)
+  const int *kp_val;      // [nkb * (npanels + 1)] first tvals value of (kb, panel)
+  const int *tcols;
+  const float *tvals;
+  int tkb;                // B rows per K block
+  int tnkb;               // K blocks
+  int tppb;               // panels per workgroup
+  int tnrb;               // row blocks
+  int tstage_cols;        // most slots of one (row block, K block) unit
+  int tstage_vals;        // most values of one unit
+  int tstage_segs;        // most sub-segments of one unit
+  long long nslots;       // slots of the whole plan
+  float *work;            // split-K partial sums (plan workspace), or null
+  long long work_floats;  // its size in floats
 };
 
 // Everything a pattern body needs for one (segment, wave) range.
@@ -119,37 +142,75 @@ __device__ __forceinline__ void store_c(float *dst, const float (&v)[V], int acc
   }
 }
 
-// The panel kernel.  D is the generated dispatcher: D::run<KM, V>(mask, acc,
-// args) runs the straight-line body of the pattern whose row mask is `mask`.
-// blockDim.x = 64 * W; dynamic LDS = W * KM * L * V floats when W > 1.
-template <int KM, int V, class D>
-__global__ void __launch_bounds__(1024) panel_kernel(DevView v, const float *__restrict__ B,
-                                                      float *__restrict__ C, int N, int L,
-                                                      int accumulate, int pack) {
+// Copy n elements global -> LDS with every thread keeping UNR loads in flight
+// (a plain strided loop waits for each load before the next).
+// Loads past the end re-read element n-1 (in bounds) so that the registers
+// are written unconditionally; only the stores are guarded.
+template <int UNR, class T>
+__device__ __forceinline__ void stage_copy(T *dst, const T *__restrict__ src, int n) {
+  if (n <= 0) return;
+  const int step = blockDim.x;
+  for (int base = threadIdx.x; base < n; base += step * UNR) {
+    T r[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) r[u] = src[min(base + u * step, n - 1)];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u)
+      if (base + u * step < n) dst[base + u * step] = r[u];
+  }
+}
+
+// The panel kernel (any N; lane groups of L lanes per slot, S = 64/L slots
+// in flight per wave).  D is the generated dispatcher: D::run<KM, V>(mask,
+// acc, args) runs the straight-line body of the pattern whose row mask is
+// `mask`.  blockDim.x = 64 * W.  With STAGE the panel's columns and values
+// are first copied to LDS (batched loads), and the same LDS is reused for the
+// cross-wave reduction.
+template <int KM, int V, bool STAGE, class D>
+__global__ void __launch_bounds__(1024)
+    panel_kernel(const int4 *__restrict__ seg, const int *__restrict__ panel_seg,
+                 const int *__restrict__ panel_slot, const int *__restrict__ panel_val,
+                 const int *__restrict__ cols, const float *__restrict__ vals,
+                 const float *__restrict__ B, float *__restrict__ C, int M, int N, int L,
+                 int accumulate, int pack, int stage_cols) {
   extern __shared__ float red[];
   const int panel = blockIdx.x;
   const int W = blockDim.x >> 6;
-  const int w = threadIdx.x >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int S = 64 / L;
   const int g = lane & (L - 1);
   const int s = lane / L;
-  const int p0 = v.panel_slot[panel];
-  const int p1 = v.panel_slot[panel + 1];
+  const int p0 = panel_slot[panel];
+  const int p1 = panel_slot[panel + 1];
   // pack-aligned share of the panel's slots for this wave
   const int npk = (p1 - p0 + pack - 1) / pack;
   const int per = ((npk + W - 1) / W) * pack;
   const int a0 = p0 + w * per;
   const int a1 = min(p1, a0 + per);
-  const int sg0 = v.panel_seg[panel];
-  const int sg1 = v.panel_seg[panel + 1];
+  const int sg0 = panel_seg[panel];
+  const int sg1 = panel_seg[panel + 1];
   const int row0 = panel * KM;
   const int LV = L * V;
+  const int *cs = cols;
+  const float *vs = vals;
+  auto stage = [&]() {
+    const int q0 = panel_val[panel];
+    const int q1 = panel_val[panel + 1];
+    int *lc = reinterpret_cast<int *>(red);
+    float *lv = red + stage_cols;
+    stage_copy<4>(lc, cols + p0, p1 - p0);
+    stage_copy<8>(lv, vals + q0, q1 - q0);
+    __syncthreads();
+    cs = lc - p0;  // indexed with global slot numbers
+    vs = lv - q0;
+  };
+  if constexpr (STAGE) stage();
   for (int cbase = 0; cbase < N; cbase += LV) {
     const int c0 = cbase + g * V;
     SegArgs args;
-    args.cols = v.cols;
-    args.vals = v.vals;
+    args.cols = cs;
+    args.vals = vs;
     args.Bc = B + c0;
     args.N = N;
     args.s = s;
@@ -161,7 +222,7 @@ __global__ void __launch_bounds__(1024) panel_kernel(DevView v, const float *__r
 #pragma unroll
       for (int e = 0; e < V; ++e) acc[r][e] = 0.f;
     for (int si = sg0; si < sg1; ++si) {
-      const int4 sd = v.seg[si];
+      const int4 sd = seg[si];
       const int lo = max(sd.y, a0);
       const int hi = min(sd.y + sd.z, a1);
       if (lo < hi) {
@@ -177,9 +238,10 @@ __global__ void __launch_bounds__(1024) panel_kernel(DevView v, const float *__r
       if (s == 0 && c0 < N) {
 #pragma unroll
         for (int r = 0; r < KM; ++r)
-          if (row0 + r < v.M) store_c<V>(C + (size_t)(row0 + r) * N + c0, acc[r], accumulate);
+          if (row0 + r < M) store_c<V>(C + (size_t)(row0 + r) * N + c0, acc[r], accumulate);
       }
     } else {
+      if constexpr (STAGE) __syncthreads();  // every wave is done with the staged stream
       if (s == 0) {
 #pragma unroll
         for (int r = 0; r < KM; ++r)
@@ -194,12 +256,15 @@ __global__ void __launch_bounds__(1024) panel_kernel(DevView v, const float *__r
         for (int ww = 0; ww < W; ++ww) sum += red[(ww * KM + r) * LV + c];
         const int row = row0 + r;
         const int col = cbase + c;
-        if (row < v.M && col < N) {
+        if (row < M && col < N) {
           float *dst = C + (size_t)row * N + col;
           *dst = accumulate ? *dst + sum : sum;
         }
       }
       __syncthreads();
+      if constexpr (STAGE) {
+        if (cbase + LV < N) stage();  // the reduction overwrote the stream
+      }
     }
   }
 }
@@ -279,8 +344,8 @@ __global__ void __launch_bounds__(1024)
     const int q1 = panel_val[panel + 1];
     int *lc = reinterpret_cast<int *>(smem);
     float *lv = smem + stage_cols;
-    for (int t = threadIdx.x; t < p1 - p0; t += blockDim.x) lc[t] = cols[p0 + t];
-    for (int t = threadIdx.x; t < q1 - q0; t += blockDim.x) lv[t] = vals[q0 + t];
+    stage_copy<4>(lc, cols + p0, p1 - p0);
+    stage_copy<8>(lv, vals + q0, q1 - q0);
     __syncthreads();
     cs = lc - p0;  // indexed with global slot numbers
     vs = lv - q0;
@@ -343,12 +408,203 @@ __global__ void __launch_bounds__(1024)
         const int q1 = panel_val[panel + 1];
         int *lc = reinterpret_cast<int *>(smem);
         float *lv = smem + stage_cols;
-        for (int t = threadIdx.x; t < p1 - p0; t += blockDim.x) lc[t] = cols[p0 + t];
-        for (int t = threadIdx.x; t < q1 - q0; t += blockDim.x) lv[t] = vals[q0 + t];
+        stage_copy<4>(lc, cols + p0, p1 - p0);
+        stage_copy<8>(lv, vals + q0, q1 - q0);
         __syncthreads();
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Tiled path (N a multiple of 64, enough reuse): split-K with B in LDS.
+// A workgroup of W waves owns (row block of ppb panels, K block of KB B rows,
+// N chunk of 64V columns).  It stages B[k0:k0+KB, n0:n0+64V] in LDS once,
+// and the unit's slots (contiguous in the plan's K-block-major copy of the
+// stream) next to it; each wave then runs its panels' sub-segments with B
+// rows read from LDS.  Every staged B row is reused by all panels of the
+// block that touch it instead of being gathered from L2 once per slot.  With
+// more than one K block the units write partial sums to the plan's
+// workspace, summed in a fixed order by splitk_reduce (deterministic).
+// ---------------------------------------------------------------------------
+struct TileArgs {
+  const int *cols;     // slot columns, indexed with tcols positions
+  const float *vals;   // values, indexed with tvals positions
+  const char *lds;     // B tile, 64 * V floats per row
+  int k0;              // first B row of the tile
+  unsigned lane_off;   // lane * V * 4 bytes
+  int lo, hi;          // slot range of the sub-segment
+  int sb, vb;          // its first slot / first value
+};
+
+template <int V>
+__device__ __forceinline__ void load_tile(float (&b)[V], const TileArgs &a, int col) {
+  constexpr unsigned row_bytes = 64u * V * 4u;
+  const float *p = reinterpret_cast<const float *>(a.lds + ((unsigned)(col - a.k0) * row_bytes + a.lane_off));
+  if constexpr (V == 4) {
+    const float4 t = *reinterpret_cast<const float4 *>(p);
+    b[0] = t.x;
+    b[1] = t.y;
+    b[2] = t.z;
+    b[3] = t.w;
+  } else if constexpr (V == 2) {
+    const float2 t = *reinterpret_cast<const float2 *>(p);
+    b[0] = t.x;
+    b[1] = t.y;
+  } else {
+    b[0] = *p;
+  }
+}
+
+// One workgroup per (row block, K block, N chunk).  LDS: the B tile
+// (KB x 64V floats) followed, with STAGE_A, by the unit's slot columns and
+// values (one contiguous range of the K-block-major stream).
+template <int KM, int V, bool STAGE_A, class D>
+__global__ void __launch_bounds__(1024)
+    tiled_kernel(const int4 *__restrict__ tseg, const int *__restrict__ kp_seg,
+                 const int *__restrict__ kp_slot, const int *__restrict__ kp_val,
+                 const int *__restrict__ tcols, const float *__restrict__ tvals,
+                 const float *__restrict__ B, float *__restrict__ C, float *__restrict__ work,
+                 int M, int K, int N, int npanels, int ppb, int KB, int stage_cols, int stage_vals,
+                 int accumulate, int direct) {
+  extern __shared__ float4 tile4[];
+  constexpr int NC = 64 * V;
+  const int rb = blockIdx.x;
+  const int kb = blockIdx.y;
+  const int n0 = blockIdx.z * NC;
+  const int k0 = kb * KB;
+  const int k1 = min(K, k0 + KB);
+  const int pf = rb * ppb;
+  const int pl = min(npanels, pf + ppb);
+  const int kbase = kb * (npanels + 1);
+  const int s0 = kp_slot[kbase + pf];
+  const int s1 = kp_slot[kbase + pl];
+  const int q0 = kp_val[kbase + pf];
+  const int q1 = kp_val[kbase + pl];
+  constexpr int q4 = NC / 4;
+  const int nq = (k1 - k0) * q4;
+  for (int base = threadIdx.x; base < nq; base += blockDim.x * 8) {
+    float4 r8[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int idx = min(base + u * (int)blockDim.x, nq - 1);  // nq >= 1: K block non-empty
+      const int r = idx / q4;
+      const int c = idx - r * q4;
+      r8[u] = *reinterpret_cast<const float4 *>(B + (size_t)(k0 + r) * N + n0 + c * 4);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (base + u * blockDim.x < nq) tile4[base + u * blockDim.x] = r8[u];
+  }
+  const int *cs = tcols;
+  const float *vs = tvals;
+  const int4 *ds = tseg;
+  if constexpr (STAGE_A) {
+    // after the B tile as allocated: sub-segment descriptors, columns, values
+    const int d0u = kp_seg[kbase + pf];
+    const int d1u = kp_seg[kbase + pl];
+    int4 *ld = reinterpret_cast<int4 *>(tile4 + min(KB, K) * q4);
+    stage_copy<4>(ld, tseg + d0u, d1u - d0u);
+    int *lc = reinterpret_cast<int *>(ld + (d1u - d0u));
+    float *lv = reinterpret_cast<float *>(lc + stage_cols);
+    stage_copy<4>(lc, tcols + s0, s1 - s0);
+    stage_copy<8>(lv, tvals + q0, q1 - q0);
+    cs = lc - s0;
+    vs = lv - q0;
+    ds = ld - d0u;
+    (void)stage_vals;
+  }
+  __syncthreads();
+  const int W = blockDim.x >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  TileArgs args;
+  args.cols = cs;
+  args.vals = vs;
+  args.lds = reinterpret_cast<const char *>(tile4);
+  args.k0 = k0;
+  args.lane_off = (unsigned)(lane * V * sizeof(float));
+  for (int panel = pf + w; panel < pl; panel += W) {
+    float acc[KM][V];
+#pragma unroll
+    for (int r = 0; r < KM; ++r)
+#pragma unroll
+      for (int e = 0; e < V; ++e) acc[r][e] = 0.f;
+    const int d0 = kp_seg[kbase + panel];
+    const int d1 = kp_seg[kbase + panel + 1];
+    for (int d = d0; d < d1; ++d) {
+      const int4 sd = ds[d];
+      args.lo = sd.y;
+      args.hi = sd.y + sd.z;
+      args.sb = sd.y;
+      args.vb = sd.w;
+      D::template run_tile<KM, V>(sd.x, acc, args);
+    }
+    const int row0 = panel * KM;
+#pragma unroll
+    for (int r = 0; r < KM; ++r) {
+      if (row0 + r >= M) break;
+      if (direct)
+        store_c<V>(C + (size_t)(row0 + r) * N + n0 + lane * V, acc[r], accumulate);
+      else
+        store_c<V>(work + ((size_t)kb * M + row0 + r) * N + n0 + lane * V, acc[r], 0);
+    }
+  }
+}
+
+// C = sum over K blocks of the partials (fixed order), + C when accumulating.
+template <int UNUSED = 0>  // template: defined in every unit that includes this header
+__global__ void __launch_bounds__(256) splitk_reduce(const float4 *__restrict__ work,
+                                                     float4 *__restrict__ C, long long n4, int nkb,
+                                                     int accumulate) {
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n4;
+       i += (long long)gridDim.x * blockDim.x) {
+    float4 s = work[i];
+    for (int k = 1; k < nkb; ++k) {
+      const float4 t = work[(size_t)k * n4 + i];
+      s.x += t.x;
+      s.y += t.y;
+      s.z += t.z;
+      s.w += t.w;
+    }
+    if (accumulate) {
+      const float4 o = C[i];
+      s.x += o.x;
+      s.y += o.y;
+      s.z += o.z;
+      s.w += o.w;
+    }
+    C[i] = s;
+  }
+}
+
+constexpr size_t kLdsBytes = 160 * 1024;  // LDS per workgroup on gfx950
+
+struct TileGeometry {
+  bool use = false;
+  bool stage_a = false;
+  int V = 0;        // floats per lane (64 * V columns per chunk)
+  int chunks = 0;   // N chunks
+  int W = 16;       // waves per workgroup
+  size_t lds = 0;
+  long long work_floats = 0;
+};
+
+inline TileGeometry tile_geometry(const DevView &v, int N) {
+  TileGeometry t;
+  if (!v.tseg || N % 64 != 0 || v.npanels <= 0) return t;
+  const int V = (N % 128 == 0) ? 2 : 1;
+  const size_t btile = (size_t)std::min(v.tkb, v.K) * 64 * V * sizeof(float);
+  if (btile > kLdsBytes) return t;
+  t.use = true;
+  t.V = V;
+  t.chunks = N / (64 * V);
+  t.W = std::min(16, std::max(1, v.tppb));
+  const size_t abytes = ((size_t)v.tstage_cols + (size_t)v.tstage_vals) * 4 + (size_t)v.tstage_segs * 16;
+  t.stage_a = btile + abytes <= kLdsBytes;
+  t.lds = btile + (t.stage_a ? abytes : 0);
+  t.work_floats = v.tnkb > 1 ? (long long)v.tnkb * v.M * N : 0;
+  return t;
 }
 
 // Floats per lane of the wide path for N columns, 0 if N does not fit it.
@@ -400,7 +656,17 @@ inline Geometry geometry(int km, int N, int W, long long K = 0, int max_pslots =
   const int groups = (N + g.V - 1) / g.V;
   g.L = 1;
   while (g.L < groups && g.L < 64) g.L <<= 1;
-  g.lds = W > 1 ? (size_t)W * km * g.L * g.V * sizeof(float) : 0;
+  const size_t red = W > 1 ? (size_t)W * km * g.L * g.V * sizeof(float) : 0;
+  g.lds = red;
+  if (max_pslots >= 0) {
+    const int sc = (max_pslots + 3) / 4 * 4;
+    const size_t st = ((size_t)sc + (size_t)max_pvals) * 4;
+    if (st <= kStageLimit) {
+      g.stage = true;
+      g.stage_cols = sc;
+      g.lds = st > red ? st : red;
+    }
+  }
   return g;
 }
 
@@ -408,6 +674,31 @@ template <int KM, class D>
 hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int accumulate, int W,
                          int pack, hipStream_t stream) {
   if (v.npanels <= 0 || N <= 0) return hipSuccess;
+  const TileGeometry tg = tile_geometry(v, N);
+  if (tg.use && (v.tnkb == 1 || (v.work && v.work_floats >= tg.work_floats))) {
+    dim3 tgrid((unsigned)v.tnrb, (unsigned)v.tnkb, (unsigned)tg.chunks), tblock((unsigned)(64 * tg.W));
+    const int direct = v.tnkb == 1;
+#define SC_TILED(VV, SA)                                                                             \
+  hipLaunchKernelGGL((tiled_kernel<KM, VV, SA, D>), tgrid, tblock, tg.lds, stream, v.tseg, v.kp_seg, \
+                     v.kp_slot, v.kp_val, v.tcols, v.tvals, B, C, v.work, v.M, v.K, N, v.npanels,   \
+                     v.tppb, v.tkb, v.tstage_cols, v.tstage_vals, accumulate, direct)
+    if (tg.V == 2) {
+      if (tg.stage_a) SC_TILED(2, true);
+      else SC_TILED(2, false);
+    } else {
+      if (tg.stage_a) SC_TILED(1, true);
+      else SC_TILED(1, false);
+    }
+#undef SC_TILED
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || direct) return e;
+    const long long n4 = (long long)v.M * N / 4;
+    const int blocks = (int)std::min<long long>(4096, (n4 + 255) / 256);
+    hipLaunchKernelGGL(splitk_reduce<0>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       reinterpret_cast<const float4 *>(v.work), reinterpret_cast<float4 *>(C), n4,
+                       v.tnkb, accumulate);
+    return hipGetLastError();
+  }
   const Geometry g = geometry(KM, N, W, v.K, v.max_pslots, v.max_pvals);
   dim3 grid((unsigned)v.npanels), block((unsigned)(64 * W));
   if (g.wide) {
@@ -427,20 +718,20 @@ hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int 
 #undef SC_WIDE
     return hipGetLastError();
   }
-  switch (g.V) {
-    case 4:
-      hipLaunchKernelGGL((panel_kernel<KM, 4, D>), grid, block, g.lds, stream, v, B, C, N, g.L,
-                         accumulate, pack);
-      break;
-    case 2:
-      hipLaunchKernelGGL((panel_kernel<KM, 2, D>), grid, block, g.lds, stream, v, B, C, N, g.L,
-                         accumulate, pack);
-      break;
-    default:
-      hipLaunchKernelGGL((panel_kernel<KM, 1, D>), grid, block, g.lds, stream, v, B, C, N, g.L,
-                         accumulate, pack);
-      break;
+#define SC_NARROW(VV, ST)                                                                          \
+  hipLaunchKernelGGL((panel_kernel<KM, VV, ST, D>), grid, block, g.lds, stream, v.seg, v.panel_seg,  \
+                     v.panel_slot, v.panel_val, v.cols, v.vals, B, C, v.M, N, g.L, accumulate, pack, \
+                     g.stage_cols)
+  if (g.stage) {
+    if (g.V == 4) SC_NARROW(4, true);
+    else if (g.V == 2) SC_NARROW(2, true);
+    else SC_NARROW(1, true);
+  } else {
+    if (g.V == 4) SC_NARROW(4, false);
+    else if (g.V == 2) SC_NARROW(2, false);
+    else SC_NARROW(1, false);
   }
+#undef SC_NARROW
   return hipGetLastError();
 }
 

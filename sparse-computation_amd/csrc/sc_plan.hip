@@ -57,6 +57,8 @@ const GenEntry kBuiltin[] = {
     {&sc_gen_builtin_km6_record, sc_gen_builtin_km6_launch},
 };
 constexpr int kMaxBuiltinKm = 6;
+constexpr int kTileRows = 256;           // B rows per K block of the tiled kernel
+constexpr double kTileMinReuse = 3.0;    // slots per staged B row to build the tiled copy
 
 void hip_check(hipError_t e, const char *what) {
   if (e != hipSuccess) throw sc::Error{SC_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e)};
@@ -73,6 +75,10 @@ struct sc_plan {
   bool dropped_pad = false;  // padding slots omitted on the device
   std::vector<uint32_t> masks;  // row masks of the patterns holding slots
   void *dmem = nullptr;  // one allocation holding every array
+  // split-K partial sums of the tiled kernel: grown on the first call that
+  // needs more (so that call must not be inside a HIP graph capture)
+  mutable float *work = nullptr;
+  mutable long long work_floats = 0;
   sc::DevView view{};
   GenEntry gen{};
 };
@@ -173,6 +179,68 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   panel_slot[(size_t)npanels] = (int32_t)cols.size();
   panel_val[(size_t)npanels] = (int32_t)vals.size();
 
+  // K-block-major copy for the tiled kernel (opt-in: on the 4096^2, N=128
+  // workload it measured slower than the wide kernel), built when each B row
+  // staged in LDS would be used by enough slots (the ratio does not depend on N).
+  const int tkb = kTileRows;
+  const int tnkb = K > 0 ? (K + tkb - 1) / tkb : 0;
+  int tnrb = 0, tppb = 0;
+  bool tiled = false;
+  if (tnkb > 0 && npanels > 0 && !cols.empty() && (flags & SC_PLAN_TILED)) {
+    tnrb = std::max(1, std::min(npanels, 512 / tnkb));
+    tppb = (npanels + tnrb - 1) / tnrb;
+    tnrb = (npanels + tppb - 1) / tppb;
+    const double staged = (double)tnrb * tnkb * std::min(tkb, K);
+    tiled = (double)cols.size() >= kTileMinReuse * staged;
+  }
+  std::vector<int4> tseg;
+  std::vector<int32_t> kp_seg, kp_slot, kp_val, tcols;
+  std::vector<float> tvals;
+  int tstage_cols = 0, tstage_vals = 0, tstage_segs = 0;
+  if (tiled) {
+    kp_seg.resize((size_t)tnkb * (npanels + 1));
+    kp_slot.resize(kp_seg.size());
+    kp_val.resize(kp_seg.size());
+    tcols.reserve(cols.size());
+    tvals.reserve(vals.size());
+    std::vector<int32_t> cursor(seg.size());  // next slot of every segment
+    for (size_t si = 0; si < seg.size(); ++si) cursor[si] = seg[si].y;
+    for (int kb = 0; kb < tnkb; ++kb) {
+      const int64_t klim = (int64_t)(kb + 1) * tkb;
+      const size_t base = (size_t)kb * (npanels + 1);
+      for (int32_t q = 0; q < npanels; ++q) {
+        kp_seg[base + q] = (int32_t)tseg.size();
+        kp_slot[base + q] = (int32_t)tcols.size();
+        kp_val[base + q] = (int32_t)tvals.size();
+        for (int32_t si = panel_seg[(size_t)q]; si < panel_seg[(size_t)q + 1]; ++si) {
+          const int4 sd = seg[(size_t)si];
+          const int pop = __builtin_popcount((unsigned)sd.x);
+          const int lo = cursor[(size_t)si];
+          int hi = lo;
+          while (hi < sd.y + sd.z && cols[(size_t)hi] < klim) ++hi;
+          if (hi == lo) continue;
+          cursor[(size_t)si] = hi;
+          tseg.push_back(make_int4(sd.x, (int)tcols.size(), hi - lo, (int)tvals.size()));
+          tcols.insert(tcols.end(), cols.begin() + lo, cols.begin() + hi);
+          const size_t v0 = (size_t)sd.w + (size_t)(lo - sd.y) * pop;
+          tvals.insert(tvals.end(), vals.begin() + v0, vals.begin() + v0 + (size_t)(hi - lo) * pop);
+        }
+      }
+      kp_seg[base + npanels] = (int32_t)tseg.size();
+      kp_slot[base + npanels] = (int32_t)tcols.size();
+      kp_val[base + npanels] = (int32_t)tvals.size();
+      for (int rb = 0; rb < tnrb; ++rb) {
+        const int pf = rb * tppb, pl = std::min(npanels, pf + tppb);
+        tstage_cols = std::max(tstage_cols, kp_slot[base + pl] - kp_slot[base + pf]);
+        tstage_vals = std::max(tstage_vals, kp_val[base + pl] - kp_val[base + pf]);
+        tstage_segs = std::max(tstage_segs, kp_seg[base + pl] - kp_seg[base + pf]);
+      }
+    }
+    tstage_cols = (tstage_cols + 3) / 4 * 4;
+    for (size_t si = 0; si < seg.size(); ++si)
+      if (cursor[si] != seg[si].y + seg[si].z) throw sc::Error{SC_ERR_INTERNAL, "tiled layout lost slots"};
+  }
+
   auto plan = std::make_unique<sc_plan>();
   hip_check(hipGetDevice(&plan->device), "hipGetDevice");
   plan->M = M;
@@ -199,13 +267,25 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   size_t off_pval = align_up<int>(off_pslot + panel_slot.size() * sizeof(int32_t));
   size_t off_cols = align_up<int>(off_pval + panel_val.size() * sizeof(int32_t));
   size_t off_vals = align_up<int>(off_cols + cols.size() * sizeof(int32_t));
-  size_t total = align_up<int>(off_vals + vals.size() * sizeof(float));
+  size_t off_tseg = align_up<int>(off_vals + vals.size() * sizeof(float));
+  size_t off_kpseg = align_up<int>(off_tseg + tseg.size() * sizeof(int4));
+  size_t off_kpslot = align_up<int>(off_kpseg + kp_seg.size() * sizeof(int32_t));
+  size_t off_kpval = align_up<int>(off_kpslot + kp_slot.size() * sizeof(int32_t));
+  size_t off_tcols = align_up<int>(off_kpval + kp_val.size() * sizeof(int32_t));
+  size_t off_tvals = align_up<int>(off_tcols + tcols.size() * sizeof(int32_t));
+  size_t total = align_up<int>(off_tvals + tvals.size() * sizeof(float));
   hip_check(hipMalloc(&plan->dmem, total), "hipMalloc(plan)");
   std::vector<unsigned char> host(total, 0);
   std::memcpy(host.data() + off_seg, seg.data(), seg.size() * sizeof(int4));
   std::memcpy(host.data() + off_pseg, panel_seg.data(), panel_seg.size() * sizeof(int32_t));
   std::memcpy(host.data() + off_pslot, panel_slot.data(), panel_slot.size() * sizeof(int32_t));
   std::memcpy(host.data() + off_pval, panel_val.data(), panel_val.size() * sizeof(int32_t));
+  std::memcpy(host.data() + off_tseg, tseg.data(), tseg.size() * sizeof(int4));
+  std::memcpy(host.data() + off_kpseg, kp_seg.data(), kp_seg.size() * sizeof(int32_t));
+  std::memcpy(host.data() + off_kpslot, kp_slot.data(), kp_slot.size() * sizeof(int32_t));
+  std::memcpy(host.data() + off_kpval, kp_val.data(), kp_val.size() * sizeof(int32_t));
+  std::memcpy(host.data() + off_tcols, tcols.data(), tcols.size() * sizeof(int32_t));
+  std::memcpy(host.data() + off_tvals, tvals.data(), tvals.size() * sizeof(float));
   std::memcpy(host.data() + off_cols, cols.data(), cols.size() * sizeof(int32_t));
   std::memcpy(host.data() + off_vals, vals.data(), vals.size() * sizeof(float));
   hipError_t e = hipMemcpy(plan->dmem, host.data(), total, hipMemcpyHostToDevice);
@@ -226,6 +306,22 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   plan->view.npanels = npanels;
   plan->view.max_pslots = max_pp;
   plan->view.max_pvals = max_pv;
+  plan->view.tseg = tiled ? (const int4 *)(base + off_tseg) : nullptr;
+  plan->view.kp_seg = (const int *)(base + off_kpseg);
+  plan->view.kp_slot = (const int *)(base + off_kpslot);
+  plan->view.kp_val = (const int *)(base + off_kpval);
+  plan->view.tcols = (const int *)(base + off_tcols);
+  plan->view.tvals = (const float *)(base + off_tvals);
+  plan->view.tkb = tkb;
+  plan->view.tnkb = tnkb;
+  plan->view.tppb = tppb;
+  plan->view.tnrb = tnrb;
+  plan->view.tstage_cols = tstage_cols;
+  plan->view.tstage_vals = tstage_vals;
+  plan->view.tstage_segs = tstage_segs;
+  plan->view.nslots = (long long)cols.size();
+  plan->view.work = nullptr;
+  plan->view.work_floats = 0;
   return plan.release();
 }
 
@@ -285,7 +381,19 @@ int launch(const sc_plan *p, const sc_gen_record *rec, sc_gen_launch_fn fn, cons
   int w = waves ? waves : (rec->waves ? rec->waves : auto_waves(p, N));
   if (sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals).lds > 65536)
     throw sc::Error{SC_ERR_ARG, "too many waves per panel for this N"};
-  int e = fn(&p->view, B, C, N, (flags & SC_ACCUMULATE) ? 1 : 0, w, stream);
+  sc::DevView view = p->view;
+  const sc::TileGeometry tg = sc::tile_geometry(view, N);
+  if (tg.use && tg.work_floats > p->work_floats) {
+    if (p->work) (void)hipFree(p->work);
+    p->work = nullptr;
+    p->work_floats = 0;
+    hip_check(hipMalloc((void **)&p->work, (size_t)tg.work_floats * sizeof(float)),
+              "hipMalloc(split-K workspace)");
+    p->work_floats = tg.work_floats;
+  }
+  view.work = p->work;
+  view.work_floats = p->work_floats;
+  int e = fn(&view, B, C, N, (flags & SC_ACCUMULATE) ? 1 : 0, w, stream);
   hip_check((hipError_t)e, "pattern kernel launch");
   return SC_OK;
 }
@@ -297,7 +405,7 @@ extern "C" {
 int sc_plan_create(const sc_cfmtx *cf, int32_t flags, sc_plan **out) {
   SC_GUARD([&] {
     if (!cf || !out) throw sc::Error{SC_ERR_ARG, "null argument"};
-    if (flags & ~SC_PLAN_DROP_PADDING) throw sc::Error{SC_ERR_ARG, "unknown plan flags"};
+    if (flags & ~(SC_PLAN_DROP_PADDING | SC_PLAN_TILED)) throw sc::Error{SC_ERR_ARG, "unknown plan flags"};
     *out = create_plan(sc_cfmtx_ref(cf), flags);
   });
 }
@@ -344,6 +452,7 @@ int sc_spmv(const sc_plan *plan, const float *dx, float *dy, int32_t flags, void
 void sc_plan_destroy(sc_plan *plan) {
   if (!plan) return;
   if (plan->dmem) (void)hipFree(plan->dmem);
+  if (plan->work) (void)hipFree(plan->work);
   delete plan;
 }
 

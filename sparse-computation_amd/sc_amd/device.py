@@ -10,6 +10,7 @@ from ._lib import check, lib, torch
 from .format import Cfmtx
 
 PLAN_DROP_PADDING = 1
+PLAN_TILED = 2
 ACCUMULATE = 1
 
 

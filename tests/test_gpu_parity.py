@@ -174,3 +174,31 @@ def test_spmm_wide_unstaged_dense_panels():
     C = run_spmm(A, B, 6, 1)
     err, _ = oracle_check(A, B, C)
     assert err <= REL_TOL, err
+
+
+@pytest.mark.parametrize("n", [64, 128, 256])
+@pytest.mark.parametrize("flags", [0, sc_amd.PLAN_TILED])
+def test_spmm_split_k_ragged(n, flags):
+    # 2050 x 3001: K not a multiple of the B tile, M not a multiple of the
+    # row block; with PLAN_TILED enough reuse for the split-K LDS-tiled kernel
+    A, B = synth_case(2050, 3001, 0.10, n, seed=0x5EED0000 + 9000 + n)
+    C = run_spmm(A, B, 4, 1, flags=flags)
+    err, _ = oracle_check(A, B, C)
+    assert err <= REL_TOL, (n, err)
+    C0 = sc_amd.synth_dense(2050 * n, 17).reshape(2050, n)
+    Cacc = run_spmm(A, B, 4, 1, flags=flags, accumulate=C0)
+    ip, ix, ax = csr_f32(A)
+    c64, cab = O.spmm_f64(2050, n, ip, ix, ax, B)
+    assert O.max_rel_err(Cacc - C0.astype(np.float64), c64, cab + np.abs(C0)) <= REL_TOL
+
+
+@pytest.mark.parametrize("flags", [0, sc_amd.PLAN_TILED])
+def test_spmm_is_deterministic(flags):
+    A, B = synth_case(4096, 4096, 0.10, 128, seed=77, structured=True)
+    cf = sc_amd.Cfmtx.build(A, 4, 1)
+    plan = sc_amd.Plan(cf, flags)
+    Bt = torch.from_numpy(B).to(DEV)
+    C1 = plan.spmm(Bt).cpu().numpy()
+    C2 = plan.spmm(Bt).cpu().numpy()
+    assert np.array_equal(C1, C2)
+    assert oracle_check(A, B, C1)[0] <= REL_TOL
