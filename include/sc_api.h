@@ -129,6 +129,10 @@ int sc_plan_create(const sc_cfmtx *cf, int32_t flags, sc_plan **out);
 /* Plan geometry: rows, cols, km, panels, device slots and values, segments. */
 int sc_plan_info(const sc_plan *plan, int32_t *m, int32_t *n, int32_t *km, int32_t *npanels,
                  int64_t *nslots, int64_t *nvals, int64_t *nsegs);
+/* Which kernel sc_spmm runs for this plan and N, and its launch geometry, as
+ * text (e.g. "wide_kernel km=4 V=2 stage=1 waves=4 grid=1024").  Diagnostic;
+ * no counterpart in the reference. */
+int sc_plan_describe(const sc_plan *plan, int32_t N, char *buf, size_t buflen);
 /* The pattern kernels: SpMMFullRowPanelGeneralKernel{km}With{kn}BlockCacheLess
  * (example_cuda/spmm_demo_gpu_utils.h:1357-1664, large N) and
  * SpmvComplexPatternDecomposeByRowSeperated (spmm_small_b_col_demo_gpu_utils.h

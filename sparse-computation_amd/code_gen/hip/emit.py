@@ -152,13 +152,15 @@ def sanitize(name: str) -> str:
 
 
 def emit_unit(name: str, km: int, patterns, kn: int = 1, waves: int = 0, variant: int = 0,
-              unroll: int = 0, origin: str = "") -> str:
+              unroll: int = 0, origin: str = "", alias: bool = False) -> str:
     """Return the text of one generated translation unit.
 
     ``patterns``: iterable of (bit string, id) in dictionary order.  Patterns
     whose length differs from ``km`` or that have no ones never match a
     panel (the format builder drops them) and get no body.
     ``variant``: 0 = any N, otherwise the only N the launcher accepts.
+    ``alias``: also export the unit as sc_gen_unit_record / sc_gen_unit_launch
+    (the fixed names the demo drivers link against).
     """
     if km < 1 or km > 20:
         raise ValueError("km must be in 1..20")
@@ -245,6 +247,16 @@ def emit_unit(name: str, km: int, patterns, kn: int = 1, waves: int = 0, variant
                f"waves, {kn}, stream);")
     out.append("}")
     out.append("")
+    if alias:
+        out.append('extern "C" __attribute__((visibility("default"))) const sc_gen_record *'
+                   f"sc_gen_unit_record = &sc_gen_{name}_record;")
+        out.append('extern "C" __attribute__((visibility("default"))) hipError_t '
+                   "sc_gen_unit_launch(const sc::DevView *v, const float *B, float *C, int N,")
+        out.append("                                                   int accumulate, int waves, "
+                   "hipStream_t stream) {")
+        out.append(f"  return sc_gen_{name}_launch(v, B, C, N, accumulate, waves, stream);")
+        out.append("}")
+        out.append("")
     return "\n".join(out)
 
 

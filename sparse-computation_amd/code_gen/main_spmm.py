@@ -36,7 +36,7 @@ def main_format(m, n, bcol_unroll_factor, warp_num, path, second_grid_dim, ptd, 
     origin = (f"main_spmm.py format m={m} n={n} bcol_unroll_factor={bcol_unroll_factor} "
               f"warp_num={warp_num} loop_order={loop_order} second_grid_dim={second_grid_dim}")
     text = emit_unit(f"spmm_km{m}_kn{n}", m, dictionary_patterns(ptd), kn=n, waves=0, variant=0,
-                     origin=origin)
+                     origin=origin, alias=True)
     write_text_to_file(text, path)
     return text
 

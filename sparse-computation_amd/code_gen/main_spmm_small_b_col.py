@@ -39,7 +39,7 @@ def main(argv=None):
     origin = (f"main_spmm_small_b_col.py m={args.m} number_of_warps={args.number_of_warps} "
               f"b_col={args.b_col}")
     text = emit_unit(f"spmm_small_km{args.m}_b{args.b_col}", args.m, dictionary_patterns(ptd),
-                     kn=1, waves=0, variant=args.b_col, origin=origin)
+                     kn=1, waves=0, variant=args.b_col, origin=origin, alias=True)
     with open(args.path, "w") as f:
         f.write(text)
     print(f"Text successfully written to {args.path}")

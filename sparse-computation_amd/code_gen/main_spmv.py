@@ -32,7 +32,7 @@ def main(argv=None):
         ptd = pdict.generate_pattern_dictionary(args.m, 1)
     origin = f"main_spmv.py m={args.m} number_of_warps={args.number_of_warps}"
     text = emit_unit(f"spmv_km{args.m}", args.m, dictionary_patterns(ptd), kn=1, waves=0,
-                     variant=1, origin=origin)
+                     variant=1, origin=origin, alias=True)
     with open(args.path, "w") as f:
         f.write(text)
     print(f"Text successfully written to {args.path}")

@@ -424,6 +424,29 @@ int sc_plan_info(const sc_plan *p, int32_t *m, int32_t *n, int32_t *km, int32_t 
   });
 }
 
+int sc_plan_describe(const sc_plan *p, int32_t N, char *buf, size_t buflen) {
+  SC_GUARD([&] {
+    if (!p || !buf || buflen == 0) throw sc::Error{SC_ERR_ARG, "null argument"};
+    if (N < 1) throw sc::Error{SC_ERR_ARG, "N must be >= 1"};
+    std::string d;
+    const sc::TileGeometry tg = sc::tile_geometry(p->view, N);
+    if (tg.use) {
+      d = "tiled_kernel km=" + std::to_string(p->km) + " V=" + std::to_string(tg.V) + " stage_a=" +
+          std::to_string(tg.stage_a ? 1 : 0) + " waves=" + std::to_string(tg.W) + " grid=" +
+          std::to_string(p->view.tnrb) + "x" + std::to_string(p->view.tnkb) + "x" + std::to_string(tg.chunks) +
+          (p->view.tnkb > 1 ? " +splitk_reduce" : "");
+    } else {
+      const int w = auto_waves(p, N);
+      const sc::Geometry g = sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals);
+      d = std::string(g.wide ? "wide_kernel" : "panel_kernel") + " km=" + std::to_string(p->km) + " V=" +
+          std::to_string(g.V) + (g.wide ? "" : " L=" + std::to_string(g.L)) + " stage=" +
+          std::to_string(g.stage ? 1 : 0) + " waves=" + std::to_string(w) + " grid=" + std::to_string(p->npanels);
+    }
+    if (d.size() + 1 > buflen) throw sc::Error{SC_ERR_ARG, "buffer too small"};
+    std::memcpy(buf, d.c_str(), d.size() + 1);
+  });
+}
+
 int sc_spmm(const sc_plan *plan, const float *dB, float *dC, int32_t N, int32_t flags,
             int32_t waves_per_panel, void *hip_stream) {
   SC_GUARD([&] {

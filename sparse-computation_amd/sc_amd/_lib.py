@@ -52,6 +52,7 @@ _SIGS = {
     "sc_spmm": ([vp, vp, vp, i32, i32, i32, vp], C.c_int),
     "sc_spmv": ([vp, vp, vp, i32, vp], C.c_int),
     "sc_plan_destroy": ([vp], None),
+    "sc_plan_describe": ([vp, i32, C.c_char_p, C.c_size_t], C.c_int),
     "sc_spmm_generated": ([vp, vp, vp, vp, vp, i32, i32, i32, vp], C.c_int),
     "sc_synth_uniform": ([i32, i32, C.c_double, C.c_double, u64, C.POINTER(vp)], C.c_int),
     "sc_synth_blocks": ([i32, i32, C.c_double, C.c_double, u64, C.POINTER(vp)], C.c_int),

@@ -62,6 +62,12 @@ class Plan:
         return dict(zip(("m", "n", "km", "npanels", "nslots", "nvals", "nsegs"),
                         [x.value for x in v32 + v64]))
 
+    def describe(self, N: int) -> str:
+        """Kernel and launch geometry sc_spmm uses for N columns."""
+        buf = C.create_string_buffer(256)
+        check(lib().sc_plan_describe(self._h, N, buf, len(buf)))
+        return buf.value.decode()
+
     @staticmethod
     def _check_operand(t, rows, cols, name):
         if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()):
