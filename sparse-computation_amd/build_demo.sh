@@ -7,10 +7,10 @@ here="$(cd "$(dirname "$0")" && pwd)"
 kind=$1
 unit=$2
 out=$3
-make -s -C "$here/csrc" ../lib/libsc.so
+make -s -C "$here/csrc" ../lib/libsc.so ../lib/libsc_vendor.so
 HIPCC=${HIPCC:-/opt/rocm/bin/hipcc}
 "$HIPCC" --offload-arch=gfx950 -O3 -std=c++17 -Xclang -target-feature -Xclang -packed-fp32-ops \
   -Wno-unused-command-line-argument -I"$here/csrc" -I"$here/../include" -DSC_DEMO_KIND="$kind" \
-  "$here/demos/demo_gpu.hip" "$unit" -L"$here/lib" -lsc -Wl,-rpath,"$here/lib" -o "$out" 2>&1 \
+  "$here/demos/demo_gpu.hip" "$unit" -L"$here/lib" -lsc -lsc_vendor -Wl,-rpath,"$here/lib" -o "$out" 2>&1 \
   | grep -v "packed-fp32-ops' is not a recognized feature" || true
 test -x "$out"

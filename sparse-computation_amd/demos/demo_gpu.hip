@@ -18,8 +18,12 @@
 // unseeded rand(); the correctness reference is the fp64 product on the host
 // (the reference compares with cuSPARSE), and Correct is 1 when the max error
 // normalised by (|A| |B|)_ij is <= 1e-5 while Error keeps the reference's
-// inf-norm of the difference; --baseline adds the single-thread CPU
-// spmm_csr_float row instead of the cuBLAS/cuSPARSE rows.
+// inf-norm of the difference.  --baseline adds the vendor-library rows of
+// the reference in its order, on this platform's libraries (libsc_vendor:
+// hipBLAS Sgemm for "CuBlas", hipBLAS fp16 GemmEx for "CuBlas Half Tensor",
+// hipBLAS fp32 GemmEx for "CuBlas GemmX", rocSPARSE for "CuSparse"; gfx950
+// has no TF32, so the "GemmX Tensor Float" row is not printed), then the
+// single-thread CPU spmm_csr_float row.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -35,6 +39,7 @@
 
 #include "sc_api.h"
 #include "sc_synth.h"
+#include "sc_vendor.h"
 
 #ifndef SC_DEMO_KIND
 #define SC_DEMO_KIND 0
@@ -238,12 +243,12 @@ int main(int argc, char **argv) {
 #if SC_DEMO_KIND == 2
   const int N = 1;
   const int trials = 20;
-  const char *op_name = "SpMV Complex Pattern Decompose By Row Seperated";
+  const char *op_name = "SpMV Compressed Format";  // spmv_demo_gpu.cu:124
   const char *exp_name = "SpMV_Demo";
 #elif SC_DEMO_KIND == 1
   const int N = cfg.bCols;
   const int trials = 7;
-  const char *op_name = "SpMM Mixed Pattern Decompose By Row Seperated";
+  const char *op_name = "SpMM Format Pack Block Cache less";  // spmm_small_b_col_demo_gpu.cu
   const char *exp_name = "SpMM_Demo";
 #else
   const int N = cfg.bCols;
@@ -311,6 +316,40 @@ int main(int argc, char **argv) {
     gpu.push_back(t);
   }
 
+  // One vendor-library row: set-up outside the timer, the library call alone
+  // between the events (the reference's execute() brackets), result checked
+  // like the pattern kernel's.
+  auto vendor_trials = [&](int vkind, int alg) {
+    std::vector<Trial> out;
+    sc_vendor *h = nullptr;
+    if (sc_vendor_create(A, vkind, N, alg, &h) != SC_OK ||
+        sc_vendor_bind(h, dB, dC, nullptr) != SC_OK || sc_vendor_run(h, nullptr) != SC_OK) {
+      std::fprintf(stderr, "vendor baseline %d: %s\n", vkind, sc_vendor_last_error());
+      if (h) sc_vendor_destroy(h);
+      return out;
+    }
+    HIP_OK(hipDeviceSynchronize());
+    std::vector<float> Cv((size_t)M * N);
+    for (int tr = 0; tr < trials; ++tr) {
+      HIP_OK(hipEventRecord(e0, nullptr));
+      if (sc_vendor_run(h, nullptr) != SC_OK) {
+        std::fprintf(stderr, "vendor baseline %d: %s\n", vkind, sc_vendor_last_error());
+        break;
+      }
+      HIP_OK(hipEventRecord(e1, nullptr));
+      HIP_OK(hipEventSynchronize(e1));
+      float ms = 0;
+      HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+      if (sc_vendor_fetch(h, nullptr) != SC_OK) break;
+      HIP_OK(hipMemcpy(Cv.data(), dC, Cv.size() * sizeof(float), hipMemcpyDeviceToHost));
+      Trial t{ms * 1e-3, false, 0.0};
+      t.error = check(Cv, t.correct);
+      out.push_back(t);
+    }
+    sc_vendor_destroy(h);
+    return out;
+  };
+
   const std::string tp_header = "MatrixName,Density,nRows,nCols,NNZ,Mode,Algorithm,bCols";
   const std::string tp_row = cfg.matrixPath + "," + tostr(0.0) + "," + tostr((double)M) + "," +
                              tostr((double)K) + "," + tostr((double)nnz) + ",Random,," + std::to_string(0);
@@ -323,12 +362,38 @@ int main(int argc, char **argv) {
     std::printf("%s%s%s,kernel_n,kernel_m,b_cols,b_unroll_factor,number_of_warps\n",
                 stats_header(trials).c_str(), sp_header.c_str(), tp_header.c_str());
   if (cfg.baseline) {
-    // spmm_csr_float (example_cuda/spmm_demo_gpu_utils.h:25-36), one thread
+    auto row = [&](const char *name, const std::vector<Trial> &t) {
+      if (t.size() == (size_t)trials)
+        std::printf("%s%s%s%s\n", stats_row(name, exp_name, cfg.matrixPath, cfg.nThread, t).c_str(),
+                    sp_row.c_str(), tp_row.c_str(), suffix.str().c_str());
+    };
+#if SC_DEMO_KIND == 2
+    // example_cuda/spmv_demo_gpu.cu:150-157: cuSPARSE, then cuBLAS
+    row("SpMV rocSparse GPU", vendor_trials(SC_VENDOR_ROCSPARSE_SPMV, 0));
+    row("SpMV hipBlas GPU", vendor_trials(SC_VENDOR_HIPBLAS_SGEMM, 0));
+#else
+    // example_cuda/spmm_demo_gpu.cu:172-191: cuBLAS, Half, GemmX, (TF32), cuSPARSE
+    row("SpMM hipBlas", vendor_trials(SC_VENDOR_HIPBLAS_SGEMM, 0));
+    row("SpMM hipBlas Half Tensor", vendor_trials(SC_VENDOR_HIPBLAS_HALF, 0));
+    row("SpMM hipBlas GemmX", vendor_trials(SC_VENDOR_HIPBLAS_GEMMEX, 0));
+    row("SpMM rocSparse", vendor_trials(SC_VENDOR_ROCSPARSE_SPMM, 0));
+#endif
+    // The reference's CPU routines, one thread: spmm_csr_float
+    // (example_cuda/spmm_demo_gpu_utils.h:25-36, fp32 sums) for SpMM,
+    // spmv_csr_float (example_cuda/spmv_demo_gpu_utils.h:86-98, fp64 row
+    // sums) for SpMV.
     std::vector<Trial> cpu;
     std::vector<float> Cc((size_t)M * N);
     for (int tr = 0; tr < trials; ++tr) {
       std::fill(Cc.begin(), Cc.end(), 0.0f);
       auto t0 = std::chrono::steady_clock::now();
+#if SC_DEMO_KIND == 2
+      for (int i = 0; i < M; ++i) {
+        double sum = 0.0;
+        for (int j = ip[i]; j < ip[i + 1]; ++j) sum += (double)(float)ax[j] * B[ix[j]];
+        Cc[i] += (float)sum;
+      }
+#else
       for (int i = 0; i < M; ++i)
         for (int j = ip[i]; j < ip[i + 1]; ++j) {
           const float v = (float)ax[j];
@@ -336,13 +401,17 @@ int main(int argc, char **argv) {
           float *c = &Cc[(size_t)i * N];
           for (int k = 0; k < N; ++k) c[k] += v * b[k];
         }
+#endif
       auto t1 = std::chrono::steady_clock::now();
       Trial t{std::chrono::duration<double>(t1 - t0).count(), false, 0.0};
       t.error = check(Cc, t.correct);
       cpu.push_back(t);
     }
-    std::printf("%s%s%s%s\n", stats_row("SpMM Serial Float", exp_name, cfg.matrixPath, cfg.nThread, cpu).c_str(),
-                sp_row.c_str(), tp_row.c_str(), suffix.str().c_str());
+#if SC_DEMO_KIND == 2
+    row("SpMV Serial Float", cpu);
+#else
+    row("SpMM Serial Float", cpu);
+#endif
   }
   std::printf("%s%s%s%s\n", stats_row(op_name, exp_name, cfg.matrixPath, cfg.nThread, gpu).c_str(),
               sp_row.c_str(), tp_row.c_str(), suffix.str().c_str());

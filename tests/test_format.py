@@ -413,16 +413,28 @@ def test_errors_are_reported_not_thrown(tmp_path):
         sc_amd.Cfmtx.read(str(long_rpp))
 
 
-def test_c_abi_exports_every_declared_symbol():
+def _declared(path):
     import re
+    with open(path) as f:
+        return set(re.findall(r"\b(sc_[a-z0-9_]+)\s*\(", f.read())) - {"sc_gen_launch_fn"}
+
+
+def test_c_abi_exports_every_declared_symbol():
     root = os.path.dirname(HERE)
     declared = set()
     for h in glob.glob(os.path.join(root, "include", "*.h")):
-        with open(h) as f:
-            text = f.read()
-        declared |= set(re.findall(r"\b(sc_[a-z0-9_]+)\s*\(", text))
-    declared -= {"sc_gen_launch_fn"}
+        if os.path.basename(h) != "sc_vendor.h":
+            declared |= _declared(h)
     lib = sc_amd.lib()
     missing = [s for s in sorted(declared) if not hasattr(lib, s)]
     assert not missing, missing
-    assert declared <= set(sc_amd.EXPORTS) | {"sc_gen_launch_fn"}
+    assert declared <= set(sc_amd.EXPORTS)
+
+
+def test_vendor_library_exports_every_declared_symbol():
+    from sc_amd import vendor
+    declared = _declared(os.path.join(os.path.dirname(HERE), "include", "sc_vendor.h"))
+    assert len(declared) == 7
+    lib = vendor.vlib()
+    missing = [s for s in sorted(declared) if not hasattr(lib, s)]
+    assert not missing, missing
