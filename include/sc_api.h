@@ -117,6 +117,8 @@ void sc_cfmtx_free(sc_cfmtx *cf);
 /* Plan flags */
 #define SC_PLAN_DROP_PADDING 1 /* omit the zero-valued padding slots on the device */
 #define SC_PLAN_TILED 2        /* also build the split-K LDS-tiled copy (opt-in)    */
+#define SC_PLAN_CHUNKED 4      /* build the column splits of the chunk kernel (B
+                                  column chunks resident in LDS, N % 32 == 0)      */
 
 /* allocateAndCopyMixedFormat (example_cuda/spmm_demo_gpu_utils.h:207-245) and
  * the constructors of the generated classes SpMMMixePatternGeneralCacheLess /

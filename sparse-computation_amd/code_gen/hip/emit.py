@@ -6,7 +6,9 @@ pattern dictionary:
 * one straight-line ``__device__`` body per pattern -- the panel rows of the
   pattern are literal indices into the accumulator tile, the ``kn`` slots of a
   pack are unrolled (``kn`` B-row loads, ``pop * kn`` value loads and
-  ``pop * kn`` FMA rows per step);
+  ``pop * kn`` FMA rows per step); the lanes-over-slots body is templated on
+  where its B rows come from (global memory for the panel kernel, an LDS
+  chunk of B for the chunk kernel);
 * a dispatcher whose ``switch`` maps a segment's row mask to its body;
 * an ``extern "C"`` launcher ``sc_gen_<name>_launch`` and a parameter record
   ``sc_gen_<name>_record`` (km, kn, waves, patterns, N variant, masks), so a
@@ -45,9 +47,9 @@ def emit_body(km: int, bits: str, pid: int, kn: int, unroll: int) -> str:
     out = []
     out.append(f"// pattern id {pid}: bits {bits} -> panel rows {', '.join(map(str, rows))} "
                f"(pop {pop}), packs of {kn} slot(s)")
-    out.append("template <int V>")
+    out.append("template <int V, class A>")
     out.append(f"__device__ __forceinline__ void {body_name(bits)}(float (&acc)[{km}][V], "
-               "const sc::SegArgs &a) {")
+               "const A &a) {")
     if unroll > 1:
         out.append(f"#pragma unroll {unroll}")
     out.append(f"  for (int j = a.lo + a.s * {kn}; j < a.hi; j += a.S * {kn}) {{")
@@ -90,8 +92,12 @@ def _wide_step(rows, pop, slots, indent, loader="sc::load_row"):
 
 
 def emit_wide_body(km: int, bits: str, pid: int, kn: int, unroll_slots: int = 8) -> str:
-    """Wide-path body: the whole wave shares each slot; `unroll_slots`
-    (a multiple of kn) B-row loads in flight, then kn-slot packs for the tail."""
+    """Wide-path body: the whole wave shares each slot; full batches of
+    `unroll_slots` (a multiple of kn) B-row loads in flight, then one
+    predicated batch for the remainder of the wave's range, so the tail of a
+    segment costs one round trip instead of one per pack.  Its loads are
+    guarded by wave-uniform branches (no load past the end); skipped slots
+    keep zero rows and zero values."""
     rows = _rows(bits)
     pop = len(rows)
     U = kn * max(1, -(-unroll_slots // kn))
@@ -104,8 +110,19 @@ def emit_wide_body(km: int, bits: str, pid: int, kn: int, unroll_slots: int = 8)
            f"  for (; j + {U} <= a.hi; j += {U}) {{"]
     out += _wide_step(rows, pop, U, "    ")
     out.append("  }")
-    out.append(f"  for (; j < a.hi; j += {kn}) {{")
-    out += _wide_step(rows, pop, kn, "    ")
+    out.append("  if (j < a.hi) {")
+    out.append("    const int last = a.hi - 1 - j;  // last valid offset in this batch (< U - 1)")
+    out.append(f"    const float *vp = a.vals + a.vb + (j - a.sb) * {pop};")
+    for q in range(U):
+        out.append(f"    float b{q}[V] = {{}};")
+    for q in range(U):
+        out.append(f"    if ({q} <= last) sc::load_row<V>(b{q}, a, a.cols[j + {q}]);")
+    for q in range(U):
+        for k in range(pop):
+            out.append(f"    const float v{q}_{k} = {q} <= last ? vp[{q * pop + k}] : 0.0f;")
+    for q in range(U):
+        for k, r in enumerate(rows):
+            out.append(f"    sc::fma_row<V>(acc[{r}], v{q}_{k}, b{q});")
     out.append("  }")
     out.append("}")
     return "\n".join(out)
@@ -213,13 +230,13 @@ def emit_unit(name: str, km: int, patterns, kn: int = 1, waves: int = 0, variant
     out.append("      default: break;")
     out.append("    }")
     out.append("  }")
-    out.append("  template <int KM, int V>")
+    out.append("  template <int KM, int V, class A>")
     out.append("  __device__ __forceinline__ static void run(int mask, float (&acc)[KM][V], "
-               "const sc::SegArgs &a) {")
+               "const A &a) {")
     out.append(f"    static_assert(KM == {km}, \"dispatcher generated for km={km}\");")
     out.append("    switch (mask) {")
     for bits, pid in usable:
-        out.append(f"      case {_mask(bits)}: {body_name(bits)}<V>(acc, a); break;  // id {pid}")
+        out.append(f"      case {_mask(bits)}: {body_name(bits)}<V, A>(acc, a); break;  // id {pid}")
     out.append("      default: break;")
     out.append("    }")
     out.append("  }")

@@ -67,7 +67,15 @@ struct DevView {
   long long nslots;       // slots of the whole plan
   float *work;            // split-K partial sums (plan workspace), or null
   long long work_floats;  // its size in floats
+  int kblock_kind;        // what the K-block-major copy was built for: 0 none,
+                          // 1 the split-K tiled kernel, 2 the chunk kernel
 };
+
+// Chunk kernel: columns of B per chunk, B rows per K block (LDS tile), and
+// panels per row group (waves per workgroup).
+constexpr int kChunkCols = 32;
+constexpr int kChunkTileRows = 512;
+constexpr int kChunkPanels = 16;
 
 // Everything a pattern body needs for one (segment, wave) range.
 struct SegArgs {
@@ -97,6 +105,43 @@ __device__ __forceinline__ void load_b(float (&b)[V], const SegArgs &a, int col)
     b[1] = t.y;
   } else {
     b[0] = a.cval ? *p : 0.f;
+  }
+}
+
+// Arguments of a lanes-over-slots body whose B rows come from a chunk of B
+// resident in LDS: rows k0 .. k0+KT-1, kChunkCols columns, row-major.
+struct ChunkArgs {
+  const int *__restrict__ cols;
+  const float *__restrict__ vals;
+  const char *lds;    // the B chunk in LDS
+  int k0;             // its first B row
+  unsigned lane_off;  // column group * V * 4 bytes
+  int lo, hi;         // slot range [lo, hi) of the segment inside the tile
+  int sb;             // first slot of the segment
+  int vb;             // first value of the segment
+  int s;              // slot sub-lane
+  // sub-lanes per wave (V = 4: 8 lanes per slot); a compile-time constant so
+  // that the bodies' slot loops need no division for their trip counts
+  static constexpr int S = 64 / (kChunkCols / 4);
+};
+
+template <int V>
+__device__ __forceinline__ void load_b(float (&b)[V], const ChunkArgs &a, int col) {
+  static_assert(V == 4, "the chunk kernel runs V = 4 (ChunkArgs::S assumes it)");
+  const float *p = reinterpret_cast<const float *>(
+      a.lds + ((unsigned)(col - a.k0) * (unsigned)(kChunkCols * sizeof(float)) + a.lane_off));
+  if constexpr (V == 4) {
+    const float4 t = *reinterpret_cast<const float4 *>(p);
+    b[0] = t.x;
+    b[1] = t.y;
+    b[2] = t.z;
+    b[3] = t.w;
+  } else if constexpr (V == 2) {
+    const float2 t = *reinterpret_cast<const float2 *>(p);
+    b[0] = t.x;
+    b[1] = t.y;
+  } else {
+    b[0] = *p;
   }
 }
 
@@ -142,6 +187,19 @@ __device__ __forceinline__ void store_c(float *dst, const float (&v)[V], int acc
   }
 }
 
+// Pin a loaded value in its registers (an empty asm that may "modify" it):
+// the compiler must finish the load before this point and cannot sink the
+// load into the guarded store that uses it, which would serialise a batch of
+// loads into load-wait-store round trips.
+__device__ __forceinline__ void keep(float &x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void keep(int &x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void keep(float4 &x) {
+  asm volatile("" : "+v"(x.x), "+v"(x.y), "+v"(x.z), "+v"(x.w));
+}
+__device__ __forceinline__ void keep(int4 &x) {
+  asm volatile("" : "+v"(x.x), "+v"(x.y), "+v"(x.z), "+v"(x.w));
+}
+
 // Copy n elements global -> LDS with every thread keeping UNR loads in flight
 // (a plain strided loop waits for each load before the next).
 // Loads past the end re-read element n-1 (in bounds) so that the registers
@@ -153,7 +211,13 @@ __device__ __forceinline__ void stage_copy(T *dst, const T *__restrict__ src, in
   for (int base = threadIdx.x; base < n; base += step * UNR) {
     T r[UNR];
 #pragma unroll
-    for (int u = 0; u < UNR; ++u) r[u] = src[min(base + u * step, n - 1)];
+    for (int u = 0; u < UNR; ++u) {
+      // streamed once: non-temporal, so it does not push B rows out of L2
+      if constexpr (sizeof(T) == 4) r[u] = __builtin_nontemporal_load(&src[min(base + u * step, n - 1)]);
+      else r[u] = src[min(base + u * step, n - 1)];
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) keep(r[u]);
 #pragma unroll
     for (int u = 0; u < UNR; ++u)
       if (base + u * step < n) dst[base + u * step] = r[u];
@@ -270,6 +334,155 @@ __global__ void __launch_bounds__(1024)
 }
 
 // ---------------------------------------------------------------------------
+// Chunk path (N a multiple of kChunkCols, kn = 1 bodies): B reused from LDS.
+// A workgroup of W waves owns (row group of W panels, N chunk of kChunkCols
+// columns) and walks K in blocks of kChunkTileRows rows.  Per block it copies
+// into LDS the B tile B[k0:k0+KT, n0:n0+32] and the group's slice of the
+// K-block-major stream (columns and values of its panels' slots with a
+// column in the block, one contiguous range), then each wave runs its
+// panel's sub-segments with lanes-over-slots bodies that read columns,
+// values and B rows from LDS.  Accumulators stay in registers across the K
+// blocks, so C is written once, by one workgroup, without split-K.
+//
+// Each B row of a tile is read from L2 once per workgroup and then reused by
+// every slot of the group's panels that names it, instead of one L2 gather
+// per slot.  The N chunks of a row group are placed on one XCD (blocks are
+// dealt to the 8 XCDs round-robin) so that the group's slice of the stream
+// is fetched into that XCD's L2 once and read from there by the others.
+// ---------------------------------------------------------------------------
+// Copy B[k0:k0+rows, 4*n04 : 4*n04+kChunkCols] (row-major, row4 float4 per
+// row) into dst, UNR float4 loads in flight per thread.  Offsets are 32-bit
+// (K * N < 2^31 is checked at launch) from a uniform base.
+template <int UNR>
+__device__ __forceinline__ void stage_chunk(float4 *dst, const float4 *__restrict__ B4, int rows,
+                                            int row4, int k0, int n04) {
+  constexpr unsigned per_row = kChunkCols / 4;
+  const unsigned n = (unsigned)rows * per_row;
+  const unsigned step = blockDim.x;
+  const float4 *src = B4 + (size_t)k0 * row4 + n04;
+  for (unsigned base = threadIdx.x; base < n; base += step * UNR) {
+    float4 r[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const unsigned i = min(base + u * step, n - 1);
+      r[u] = src[(i / per_row) * (unsigned)row4 + (i % per_row)];
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) keep(r[u]);
+#pragma unroll
+    for (int u = 0; u < UNR; ++u)
+      if (base + u * step < n) dst[base + u * step] = r[u];
+  }
+}
+
+template <int KM, int V, class D>
+__global__ void __launch_bounds__(1024)
+    chunk_kernel(const int4 *__restrict__ tseg, const int *__restrict__ kp_seg,
+                 const int *__restrict__ kp_slot, const int *__restrict__ kp_val,
+                 const int *__restrict__ tcols, const float *__restrict__ tvals,
+                 const float *__restrict__ B, float *__restrict__ C, int M, int K, int N, int npanels,
+                 int ppg, int ngroups, int nchunks, int KT, int nkb, int stage_cols, int accumulate) {
+  constexpr int L = kChunkCols / V;  // lanes per slot
+  constexpr int S = 64 / L;          // slots in flight per wave
+  extern __shared__ float4 smem4[];
+  float4 *btile = smem4;
+  // the B tile holds min(KT, K) rows (the LDS size the launch allocated)
+  int *lcols = reinterpret_cast<int *>(smem4 + (size_t)min(KT, K) * (kChunkCols / 4));
+  float *lvals = reinterpret_cast<float *>(lcols + stage_cols);
+  // XCD-aware order: block b runs on XCD b % 8; the chunks of a row group
+  // share an XCD.
+  const int xcd = blockIdx.x & 7;
+  const int i = blockIdx.x >> 3;
+  const int g = (i / nchunks) * 8 + xcd;
+  const int chunk = i % nchunks;
+  if (g >= ngroups) return;  // uniform for the block, before any barrier
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int gl = lane % L;
+  const int s = lane / L;
+  const int p0 = g * ppg;
+  const int p1 = min(npanels, p0 + ppg);
+  const int panel = p0 + w;
+  const bool has_panel = panel < p1;
+  const int n0 = chunk * kChunkCols;
+
+  ChunkArgs args;
+  args.lds = reinterpret_cast<const char *>(btile);
+  args.lane_off = (unsigned)(gl * V * sizeof(float));
+  args.s = s;
+  static_assert(ChunkArgs::S == S, "lanes per slot");
+  float acc[KM][V];
+#pragma unroll
+  for (int r = 0; r < KM; ++r)
+#pragma unroll
+    for (int e = 0; e < V; ++e) acc[r][e] = 0.f;
+
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int k0 = kb * KT;
+    const int rows = min(KT, K - k0);
+    const size_t base = (size_t)kb * (npanels + 1);
+    const int us0 = kp_slot[base + p0], us1 = kp_slot[base + p1];
+    const int uv0 = kp_val[base + p0], uv1 = kp_val[base + p1];
+    if (kb > 0) __syncthreads();  // every wave is done with the previous block
+    stage_chunk<8>(btile, reinterpret_cast<const float4 *>(B), rows, N / 4, k0, n0 / 4);
+    stage_copy<4>(lcols, tcols + us0, us1 - us0);
+    stage_copy<8>(lvals, tvals + uv0, uv1 - uv0);
+    __syncthreads();
+    if (has_panel) {
+      args.cols = lcols - us0;  // indexed with positions in tcols / tvals
+      args.vals = lvals - uv0;
+      args.k0 = k0;
+      const int sg0 = kp_seg[base + panel];
+      const int sg1 = kp_seg[base + panel + 1];
+      for (int si = sg0; si < sg1; ++si) {
+        const int4 sd = tseg[si];
+        args.lo = sd.y;
+        args.hi = sd.y + sd.z;
+        args.sb = sd.y;
+        args.vb = sd.w;
+        D::template run<KM, V>(sd.x, acc, args);
+      }
+    }
+  }
+  reduce_slot_lanes<KM, V>(acc, L);
+  if (has_panel && s == 0) {
+    const int row0 = panel * KM;
+#pragma unroll
+    for (int r = 0; r < KM; ++r)
+      if (row0 + r < M) store_c<V>(C + (size_t)(row0 + r) * N + n0 + gl * V, acc[r], accumulate);
+  }
+}
+
+// Launch shape of the chunk kernel for N columns, or use = false.
+struct ChunkGeometry {
+  bool use = false;
+  int W = 0;        // waves per workgroup = panels per row group
+  int ngroups = 0;  // row groups
+  int nchunks = 0;  // N / kChunkCols
+  int KT = 0;       // B rows per LDS tile
+  unsigned grid = 0;
+  size_t lds = 0;
+};
+
+constexpr size_t kChunkLdsBytes = 160 * 1024;
+
+inline ChunkGeometry chunk_geometry(const DevView &v, int N) {
+  ChunkGeometry c;
+  if (!v.tseg || v.kblock_kind != 2 || N % kChunkCols != 0 || v.npanels <= 0 || v.K <= 0) return c;
+  if ((long long)v.K * N >= (1LL << 31)) return c;
+  c.nchunks = N / kChunkCols;
+  c.KT = v.tkb;
+  c.W = v.tppb;
+  c.ngroups = v.tnrb;
+  c.lds = (size_t)std::min(v.tkb, v.K) * kChunkCols * sizeof(float) +
+          ((size_t)v.tstage_cols + (size_t)v.tstage_vals) * sizeof(float);
+  if (c.lds > kChunkLdsBytes) return c;
+  c.grid = (unsigned)(8 * ((c.ngroups + 7) / 8) * c.nchunks);
+  c.use = true;
+  return c;
+}
+
+// ---------------------------------------------------------------------------
 // Wide path (N a multiple of 64): the whole wave works on one slot at a time,
 // lane l owning columns cbase + l*V .. + V-1.  Column indices and values are
 // then wave-uniform: they come through the scalar cache (s_load), the B-row
@@ -281,31 +494,35 @@ constexpr int UW = 8;
 struct WideArgs {
   const int *__restrict__ cols;
   const float *__restrict__ vals;
-  const char *__restrict__ Bc;  // B + cbase (wave-uniform)
-  unsigned lane_off;            // lane * V * 4 bytes
-  unsigned row_bytes;           // N * 4
+  __amdgpu_buffer_rsrc_t B;  // buffer over B + cbase (wave-uniform)
+  unsigned lane_off;         // lane * V * 4 bytes
+  unsigned row_bytes;        // N * 4
   int N;
   int lo, hi;  // slot range of this wave in the segment
   int sb, vb;  // first slot / first value of the segment
 };
 
-// 32-bit byte offsets from a uniform base (K * N * 4 < 2^32 is checked at
-// launch): the load becomes global_load saddr + voffset.
+// Buffer descriptor word 3 for gfx9-family untyped loads (32-bit data format).
+constexpr int kBufferWord3 = 0x00020000;
+
+// B-row load of the wide path: the row offset col * N * 4 (< 2^32, checked at
+// launch) goes into the scalar soffset of a buffer load and the lane's column
+// offset into voffset, so forming the address costs no vector instruction.
 template <int V>
 __device__ __forceinline__ void load_row(float (&b)[V], const WideArgs &a, int col) {
-  const float *p = reinterpret_cast<const float *>(a.Bc + ((unsigned)col * a.row_bytes + a.lane_off));
+  const unsigned soff = (unsigned)__builtin_amdgcn_readfirstlane(col) * a.row_bytes;
   if constexpr (V == 4) {
-    const float4 t = *reinterpret_cast<const float4 *>(p);
+    const float4 t = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(a.B, a.lane_off, soff, 0));
     b[0] = t.x;
     b[1] = t.y;
     b[2] = t.z;
     b[3] = t.w;
   } else if constexpr (V == 2) {
-    const float2 t = *reinterpret_cast<const float2 *>(p);
+    const float2 t = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(a.B, a.lane_off, soff, 0));
     b[0] = t.x;
     b[1] = t.y;
   } else {
-    b[0] = *p;
+    b[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(a.B, a.lane_off, soff, 0));
   }
 }
 
@@ -319,8 +536,8 @@ __global__ void __launch_bounds__(1024)
     wide_kernel(const int4 *__restrict__ seg, const int *__restrict__ panel_seg,
                 const int *__restrict__ panel_slot, const int *__restrict__ panel_val,
                 const int *__restrict__ cols, const float *__restrict__ vals,
-                const float *__restrict__ B, float *__restrict__ C, int M, int N, int accumulate,
-                int pack, int stage_cols) {
+                const float *__restrict__ B, float *__restrict__ C, int M, int K, int N,
+                int accumulate, int pack, int stage_cols) {
   extern __shared__ float smem[];
   const int panel = blockIdx.x;
   const int W = blockDim.x >> 6;
@@ -355,7 +572,10 @@ __global__ void __launch_bounds__(1024)
     WideArgs args;
     args.cols = cs;
     args.vals = vs;
-    args.Bc = reinterpret_cast<const char *>(B + cbase);
+    // bytes of B from column cbase of row 0 to the end (< 2^32, checked at launch)
+    const unsigned span = (unsigned)(((size_t)K * N - cbase) * sizeof(float));
+    args.B = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(B + cbase), (short)0, (int)span,
+                                               kBufferWord3);
     args.lane_off = (unsigned)(lane * V * sizeof(float));
     args.row_bytes = (unsigned)(N * sizeof(float));
     args.N = N;
@@ -592,7 +812,7 @@ struct TileGeometry {
 
 inline TileGeometry tile_geometry(const DevView &v, int N) {
   TileGeometry t;
-  if (!v.tseg || N % 64 != 0 || v.npanels <= 0) return t;
+  if (!v.tseg || v.kblock_kind != 1 || N % 64 != 0 || v.npanels <= 0) return t;
   const int V = (N % 128 == 0) ? 2 : 1;
   const size_t btile = (size_t)std::min(v.tkb, v.K) * 64 * V * sizeof(float);
   if (btile > kLdsBytes) return t;
@@ -699,13 +919,23 @@ hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int 
                        v.tnkb, accumulate);
     return hipGetLastError();
   }
+  if (pack == 1) {
+    const ChunkGeometry cg = chunk_geometry(v, N);
+    if (cg.use) {
+      hipLaunchKernelGGL((chunk_kernel<KM, 4, D>), dim3(cg.grid), dim3((unsigned)(64 * cg.W)), cg.lds,
+                         stream, v.tseg, v.kp_seg, v.kp_slot, v.kp_val, v.tcols, v.tvals, B, C, v.M,
+                         v.K, N, v.npanels, v.tppb, cg.ngroups, cg.nchunks, cg.KT, v.tnkb,
+                         v.tstage_cols, accumulate);
+      return hipGetLastError();
+    }
+  }
   const Geometry g = geometry(KM, N, W, v.K, v.max_pslots, v.max_pvals);
   dim3 grid((unsigned)v.npanels), block((unsigned)(64 * W));
   if (g.wide) {
 #define SC_WIDE(VV, ST)                                                                           \
   hipLaunchKernelGGL((wide_kernel<KM, VV, ST, D>), grid, block, g.lds, stream, v.seg, v.panel_seg, \
-                     v.panel_slot, v.panel_val, v.cols, v.vals, B, C, v.M, N, accumulate, pack,    \
-                     g.stage_cols)
+                     v.panel_slot, v.panel_val, v.cols, v.vals, B, C, v.M, v.K, N, accumulate,     \
+                     pack, g.stage_cols)
     if (g.stage) {
       if (g.V == 4) SC_WIDE(4, true);
       else if (g.V == 2) SC_WIDE(2, true);

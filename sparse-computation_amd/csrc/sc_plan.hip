@@ -179,19 +179,41 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   panel_slot[(size_t)npanels] = (int32_t)cols.size();
   panel_val[(size_t)npanels] = (int32_t)vals.size();
 
-  // K-block-major copy for the tiled kernel (opt-in: on the 4096^2, N=128
-  // workload it measured slower than the wide kernel), built when each B row
-  // staged in LDS would be used by enough slots (the ratio does not depend on N).
-  const int tkb = kTileRows;
+  // K-block-major copy of the stream: for K block kb and panel p, the part
+  // of each of p's segments whose columns fall in the block, contiguous per
+  // (kb, p) and so per (kb, group of panels).  Built for the split-K tiled
+  // kernel (SC_PLAN_TILED, 256-row blocks, only with enough B reuse; opt-in:
+  // on the 4096^2, N=128 workload it measured slower than the wide kernel)
+  // or for the chunk kernel (SC_PLAN_CHUNKED, 512-row blocks, groups of
+  // kChunkPanels panels).  Needs every segment in ascending column order,
+  // which is what the format builder writes; a file that is not gets no copy.
+  const bool want_tiled = (flags & SC_PLAN_TILED) != 0;
+  const bool want_chunk = (flags & SC_PLAN_CHUNKED) != 0;
+  const int tkb = want_chunk ? sc::kChunkTileRows : kTileRows;
   const int tnkb = K > 0 ? (K + tkb - 1) / tkb : 0;
   int tnrb = 0, tppb = 0;
   bool tiled = false;
-  if (tnkb > 0 && npanels > 0 && !cols.empty() && (flags & SC_PLAN_TILED)) {
+  int kind = 0;
+  bool sorted = true;
+  for (size_t si = 0; si < seg.size() && sorted; ++si)
+    for (int j = seg[si].y + 1; j < seg[si].y + seg[si].z; ++j)
+      if (cols[(size_t)j] < cols[(size_t)j - 1]) {
+        sorted = false;
+        break;
+      }
+  if (tnkb > 0 && npanels > 0 && !cols.empty() && sorted && want_tiled) {
     tnrb = std::max(1, std::min(npanels, 512 / tnkb));
     tppb = (npanels + tnrb - 1) / tnrb;
     tnrb = (npanels + tppb - 1) / tppb;
     const double staged = (double)tnrb * tnkb * std::min(tkb, K);
     tiled = (double)cols.size() >= kTileMinReuse * staged;
+    kind = tiled ? 1 : 0;
+  }
+  if (tnkb > 0 && npanels > 0 && !cols.empty() && sorted && want_chunk) {
+    tppb = std::min(npanels, sc::kChunkPanels);
+    tnrb = (npanels + tppb - 1) / tppb;
+    tiled = true;
+    kind = 2;
   }
   std::vector<int4> tseg;
   std::vector<int32_t> kp_seg, kp_slot, kp_val, tcols;
@@ -322,6 +344,7 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   plan->view.nslots = (long long)cols.size();
   plan->view.work = nullptr;
   plan->view.work_floats = 0;
+  plan->view.kblock_kind = kind;
   return plan.release();
 }
 
@@ -405,7 +428,10 @@ extern "C" {
 int sc_plan_create(const sc_cfmtx *cf, int32_t flags, sc_plan **out) {
   SC_GUARD([&] {
     if (!cf || !out) throw sc::Error{SC_ERR_ARG, "null argument"};
-    if (flags & ~(SC_PLAN_DROP_PADDING | SC_PLAN_TILED)) throw sc::Error{SC_ERR_ARG, "unknown plan flags"};
+    if (flags & ~(SC_PLAN_DROP_PADDING | SC_PLAN_TILED | SC_PLAN_CHUNKED))
+      throw sc::Error{SC_ERR_ARG, "unknown plan flags"};
+    if ((flags & SC_PLAN_TILED) && (flags & SC_PLAN_CHUNKED))
+      throw sc::Error{SC_ERR_ARG, "SC_PLAN_TILED and SC_PLAN_CHUNKED are exclusive"};
     *out = create_plan(sc_cfmtx_ref(cf), flags);
   });
 }
@@ -430,7 +456,13 @@ int sc_plan_describe(const sc_plan *p, int32_t N, char *buf, size_t buflen) {
     if (N < 1) throw sc::Error{SC_ERR_ARG, "N must be >= 1"};
     std::string d;
     const sc::TileGeometry tg = sc::tile_geometry(p->view, N);
-    if (tg.use) {
+    const sc::ChunkGeometry cg = sc::chunk_geometry(p->view, N);
+    if (!tg.use && cg.use) {
+      d = "chunk_kernel km=" + std::to_string(p->km) + " V=4 cols=" + std::to_string(sc::kChunkCols) +
+          " tile_rows=" + std::to_string(std::min(cg.KT, p->K)) + " waves=" + std::to_string(cg.W) + " grid=" +
+          std::to_string(cg.grid) + " (" + std::to_string(cg.ngroups) + " row groups x " +
+          std::to_string(cg.nchunks) + " chunks)";
+    } else if (tg.use) {
       d = "tiled_kernel km=" + std::to_string(p->km) + " V=" + std::to_string(tg.V) + " stage_a=" +
           std::to_string(tg.stage_a ? 1 : 0) + " waves=" + std::to_string(tg.W) + " grid=" +
           std::to_string(p->view.tnrb) + "x" + std::to_string(p->view.tnkb) + "x" + std::to_string(tg.chunks) +

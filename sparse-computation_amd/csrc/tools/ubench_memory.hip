@@ -1,6 +1,9 @@
 // ubench_memory.hip -- ceilings of the data paths the pattern kernels use on
 // gfx950: random 512-byte row gathers from an L2-resident table (the B-row
-// gathers of the wide kernel), LDS read bandwidth (b64/b128) and L1-hit reads.
+// gathers of the wide kernel), contiguous streaming reads from L2, the
+// strided K x Nc column-chunk reads that stage a B chunk in LDS, LDS read
+// bandwidth (b64/b128), LDS b128 reads of random rows (lanes over slots) and
+// L1-hit reads.
 // All indices are masked into their buffers; every loop has a fixed trip count.
 //   hipcc --offload-arch=gfx950 -O3 -Xclang -target-feature -Xclang -packed-fp32-ops \
 //         ubench_memory.hip -o ../../lib/ubench_memory
@@ -56,6 +59,85 @@ __global__ void lds_read(int iters, float *out) {
       }
     }
     base += 256;
+  }
+  if (acc == 1234.5f) out[0] = acc;
+}
+
+// Contiguous runs from an L2-resident buffer: per iteration each wave reads
+// U consecutive 1 KiB pieces (float4 per lane) starting at a random piece
+// (scalar xorshift), wrapping in `mask64`.
+template <int U>
+__global__ void stream_l2(const float4 *__restrict__ buf, int mask64, int iters, float *out) {
+  const int lane = threadIdx.x & 63;
+  unsigned st = 0x9E3779B9u * (blockIdx.x * 16 + (threadIdx.x >> 6) + 1);
+  st = __builtin_amdgcn_readfirstlane(st);
+  float acc = 0.f;
+  for (int it = 0; it < iters; ++it) {
+    st ^= st << 13; st ^= st >> 17; st ^= st << 5;
+    const int piece = (int)st;
+    float4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = buf[(size_t)((piece + u) & mask64) * 64 + lane];
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc += v[u].x + v[u].w;
+  }
+  if (acc == 1234.5f) out[0] = acc;
+}
+
+// Column-chunk staging: block b copies rows 0..K-1, columns [c0, c0+NC) of a
+// row-major K x 128 fp32 matrix into LDS (NC/4 lanes per row, float4 each),
+// the load pattern of a B chunk staged for lanes-over-slots kernels.
+template <int NC>
+__global__ void chunk_stage(const float4 *__restrict__ B, int K, int reps, float *out) {
+  extern __shared__ float4 lds4[];
+  const int per_row = NC / 4;
+  const int c0 = (blockIdx.x % (128 / NC)) * NC;
+  float acc = 0.f;
+  for (int r = 0; r < reps; ++r) {
+    for (int t = threadIdx.x; t < K * per_row; t += blockDim.x) {
+      const int row = t / per_row, q = t % per_row;
+      lds4[t] = B[(size_t)row * 32 + c0 / 4 + q];
+    }
+    __syncthreads();
+    acc += lds4[(threadIdx.x * 7 + r) % (K * per_row)].x;
+    __syncthreads();
+  }
+  if (acc == 1234.5f) out[0] = acc;
+}
+
+// LDS b128 reads of rows: lanes are (slot, part) with LPS lanes per slot;
+// lane q of a slot reads bytes [16q, 16q+16) of its row (row stride
+// STRIDE_F4 float4) in a 128 KiB array.  Per iteration each slot draws a
+// random start row r0 < NROWS/2 (RANDOM) or takes r0 = its slot number
+// (consecutive rows, the conflict-free control), then reads rows
+// r0 + u*NROWS/32 for u < 16 (immediate offsets, so the loop is LDS-bound).
+template <int LPS, int STRIDE_F4, int NROWS, bool RANDOM>
+__global__ void lds_rows(int iters, float *out) {
+  extern __shared__ float4 lds4[];
+  for (int t = threadIdx.x; t < NROWS * STRIDE_F4; t += blockDim.x) lds4[t] = make_float4(t, 0, 0, 0);
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int q = lane % LPS;
+  const int slot = lane / LPS;
+  unsigned st = 0x9E3779B9u * (blockIdx.x * 1024 + threadIdx.x / LPS + 1);
+  constexpr int D = NROWS / 32;
+  float acc = 0.f;
+  for (int it = 0; it < iters; ++it) {
+    int r0;
+    if constexpr (RANDOM) {
+      st ^= st << 13; st ^= st >> 17; st ^= st << 5;
+      r0 = (int)(st & (NROWS / 2 - 1));
+    } else {
+      r0 = (slot + it) & (NROWS / 2 - 1);
+    }
+    const float4 *p = lds4 + r0 * STRIDE_F4 + q;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      float4 v = p[u * D * STRIDE_F4];
+      // keep all four dwords live without spending VALU on them
+      asm volatile("" : : "v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w));
+    }
+    acc += (float)r0;
   }
   if (acc == 1234.5f) out[0] = acc;
 }
@@ -138,6 +220,72 @@ int main() {
       double bytes = 10.0 * blocks * wpb * iters * 8 * 64.0 * vec * 4;
       printf("lds b%d: %.2f TB/s (%.1f B/clk/CU)\n", vec * 32, bytes / (ms * 1e-3) / 1e12,
              bytes / (ms * 1e-3) / CUs / (prop.clockRate * 1e3));
+    }
+  }
+  {
+    // contiguous reads of the 2 MiB table (L2 resident)
+    const int blocks = CUs * 4, wpb = 8, iters = 64;  // runs of 8 KiB
+    for (int rep = -1; rep < 10; ++rep) {
+      if (rep == 0) CK(hipEventRecord(e0));
+      hipLaunchKernelGGL(stream_l2<8>, dim3(blocks), dim3(64 * wpb), 0, 0, (const float4 *)tab,
+                         (rows * 512 / 1024) - 1, iters, out);
+    }
+    CK(hipEventRecord(e1));
+    CK(hipEventSynchronize(e1));
+    float ms;
+    CK(hipEventElapsedTime(&ms, e0, e1));
+    double bytes = 10.0 * blocks * wpb * iters * 8 * 1024.0;
+    printf("contiguous 8 KiB runs from l2: %.2f TB/s (%.1f B/clk/CU)\n", bytes / (ms * 1e-3) / 1e12,
+           bytes / (ms * 1e-3) / CUs / (prop.clockRate * 1e3));
+  }
+  {
+    // column-chunk staging: K = 4096 rows of the 4096 x 128 table, NC = 8 / 16 / 32 columns
+    const int K = 4096, blocks = CUs, reps = 8;
+    struct { int nc, lds; void (*k)(const float4 *, int, int, float *); } cfgs[] = {
+        {8, 4096 * 32, chunk_stage<8>}, {16, 2048 * 64, chunk_stage<16>}, {32, 1024 * 128, chunk_stage<32>}};
+    for (auto &c : cfgs) {
+      const int Kc = c.lds / (c.nc * 4);
+      CK(hipFuncSetAttribute((const void *)c.k, hipFuncAttributeMaxDynamicSharedMemorySize, c.lds));
+      for (int rep = -1; rep < 10; ++rep) {
+        if (rep == 0) CK(hipEventRecord(e0));
+        hipLaunchKernelGGL(c.k, dim3(blocks), dim3(1024), c.lds, 0, (const float4 *)tab, Kc, reps, out);
+      }
+      CK(hipEventRecord(e1));
+      CK(hipEventSynchronize(e1));
+      float ms;
+      CK(hipEventElapsedTime(&ms, e0, e1));
+      double bytes = 10.0 * blocks * reps * (double)c.lds;
+      printf("chunk stage NC=%d (%d rows): %.2f TB/s (%.1f B/clk/CU)\n", c.nc, Kc,
+             bytes / (ms * 1e-3) / 1e12, bytes / (ms * 1e-3) / CUs / (prop.clockRate * 1e3));
+    }
+    (void)K;
+  }
+  {
+    // LDS b128 reads of random rows: 64-byte rows (NC=16, 4 lanes per slot) and
+    // 128-byte rows (NC=32, 8 lanes per slot), dense or padded by 16 bytes
+    const int blocks = CUs, wpb = 16, iters = 256;
+    struct { const char *name; int lps, stride; void (*k)(int, float *); } cfgs[] = {
+        {"64B rows, 4 lanes/slot, consecutive", 4, 4, lds_rows<4, 4, 2048, false>},
+        {"64B rows, 4 lanes/slot, random", 4, 4, lds_rows<4, 4, 2048, true>},
+        {"64B rows +16B pad, 4 lanes/slot, random", 4, 5, lds_rows<4, 5, 1024, true>},
+        {"128B rows, 8 lanes/slot, consecutive", 8, 8, lds_rows<8, 8, 1024, false>},
+        {"128B rows, 8 lanes/slot, random", 8, 8, lds_rows<8, 8, 1024, true>},
+        {"128B rows +16B pad, 8 lanes/slot, random", 8, 9, lds_rows<8, 9, 512, true>},
+        {"256B rows, 16 lanes/slot, random", 16, 16, lds_rows<16, 16, 512, true>}};
+    for (auto &c : cfgs) {
+      const int lds = 131072;
+      CK(hipFuncSetAttribute((const void *)c.k, hipFuncAttributeMaxDynamicSharedMemorySize, lds));
+      for (int rep = -1; rep < 10; ++rep) {
+        if (rep == 0) CK(hipEventRecord(e0));
+        hipLaunchKernelGGL(c.k, dim3(blocks), dim3(64 * wpb), lds, 0, iters, out);
+      }
+      CK(hipEventRecord(e1));
+      CK(hipEventSynchronize(e1));
+      float ms;
+      CK(hipEventElapsedTime(&ms, e0, e1));
+      double bytes = 10.0 * blocks * wpb * iters * 16 * 64.0 * 16;
+      printf("lds rows b128 (%s): %.2f TB/s (%.1f B/clk/CU)\n", c.name,
+             bytes / (ms * 1e-3) / 1e12, bytes / (ms * 1e-3) / CUs / (prop.clockRate * 1e3));
     }
   }
   {

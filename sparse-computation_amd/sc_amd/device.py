@@ -11,6 +11,7 @@ from .format import Cfmtx
 
 PLAN_DROP_PADDING = 1
 PLAN_TILED = 2
+PLAN_CHUNKED = 4
 ACCUMULATE = 1
 
 

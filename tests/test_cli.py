@@ -61,7 +61,7 @@ def test_python_reader_of_cfmtx():
 
 
 def _cases(text):
-    return re.findall(r"case (\d+): pattern_(\d+)<V>", text)
+    return re.findall(r"case (\d+): pattern_(\d+)<V, A>", text)
 
 
 @pytest.mark.parametrize("km,kn", [(4, 1), (4, 2), (6, 3), (1, 1)])

@@ -118,10 +118,11 @@ def test_spmm_drop_padding_plan():
     assert oracle_check(A, B, C2)[0] <= REL_TOL
 
 
+@pytest.mark.parametrize("flags", [0, sc_amd.PLAN_CHUNKED])
 @pytest.mark.parametrize("n", [1, 32, 128])
-def test_spmm_structured_4096(n):
+def test_spmm_structured_4096(n, flags):
     A, B = synth_case(4096, 4096, 0.10, n, seed=0x5EED0000 + 4000 + n, structured=True)
-    C = run_spmm(A, B, 4, 1)
+    C = run_spmm(A, B, 4, 1, flags=flags)
     err, _ = oracle_check(A, B, C)
     assert err <= REL_TOL, (n, err)
 
@@ -177,7 +178,7 @@ def test_spmm_wide_unstaged_dense_panels():
 
 
 @pytest.mark.parametrize("n", [64, 128, 256])
-@pytest.mark.parametrize("flags", [0, sc_amd.PLAN_TILED])
+@pytest.mark.parametrize("flags", [0, sc_amd.PLAN_TILED, sc_amd.PLAN_CHUNKED])
 def test_spmm_split_k_ragged(n, flags):
     # 2050 x 3001: K not a multiple of the B tile, M not a multiple of the
     # row block; with PLAN_TILED enough reuse for the split-K LDS-tiled kernel
@@ -192,7 +193,7 @@ def test_spmm_split_k_ragged(n, flags):
     assert O.max_rel_err(Cacc - C0.astype(np.float64), c64, cab + np.abs(C0)) <= REL_TOL
 
 
-@pytest.mark.parametrize("flags", [0, sc_amd.PLAN_TILED])
+@pytest.mark.parametrize("flags", [0, sc_amd.PLAN_TILED, sc_amd.PLAN_CHUNKED])
 def test_spmm_is_deterministic(flags):
     A, B = synth_case(4096, 4096, 0.10, 128, seed=77, structured=True)
     cf = sc_amd.Cfmtx.build(A, 4, 1)
@@ -202,3 +203,57 @@ def test_spmm_is_deterministic(flags):
     C2 = plan.spmm(Bt).cpu().numpy()
     assert np.array_equal(C1, C2)
     assert oracle_check(A, B, C1)[0] <= REL_TOL
+
+
+@pytest.mark.parametrize("n", [32, 64, 96, 128, 512])
+@pytest.mark.parametrize("km,kn", [(1, 1), (2, 3), (3, 1), (4, 2), (5, 1), (6, 8)])
+def test_chunk_kernel_coarsen_factors(km, kn, n):
+    # B column chunks in LDS: every km, packs with padding slots, one K tile
+    A, B = synth_case(300, 700, 0.12, n, seed=0x5EED0000 + 9500 + km * 10 + kn + n)
+    cf = sc_amd.Cfmtx.build(A, km, kn)
+    plan = sc_amd.Plan(cf, sc_amd.PLAN_CHUNKED)
+    assert plan.describe(n).startswith("chunk_kernel")
+    C = run_spmm(A, B, km, kn, flags=sc_amd.PLAN_CHUNKED)
+    err, _ = oracle_check(A, B, C)
+    assert err <= REL_TOL, (km, kn, n, err)
+
+
+def test_chunk_kernel_tiles_and_ragged_k():
+    # K = 2600: three LDS tiles, the last one partial; M ragged; accumulate
+    A, B = synth_case(1030, 2600, 0.08, 64, seed=0x5EED0000 + 9600)
+    C = run_spmm(A, B, 4, 1, flags=sc_amd.PLAN_CHUNKED)
+    assert oracle_check(A, B, C)[0] <= REL_TOL
+    C0 = sc_amd.synth_dense(1030 * 64, 18).reshape(1030, 64)
+    Cacc = run_spmm(A, B, 4, 1, flags=sc_amd.PLAN_CHUNKED, accumulate=C0)
+    ip, ix, ax = csr_f32(A)
+    c64, cab = O.spmm_f64(1030, 64, ip, ix, ax, B)
+    assert O.max_rel_err(Cacc - C0.astype(np.float64), c64, cab + np.abs(C0)) <= REL_TOL
+
+
+def test_chunk_kernel_not_used_for_unsorted_segments(tmp_path):
+    # a hand-written .cfmtx whose segment lists columns out of order: the plan
+    # builds no column splits and the kernel falls back, still correct
+    p = tmp_path / "u.cfmtx"
+    p.write_text("4 8 4 1 1\n1111 0 \n0 2\n5 1\n"
+                 "1.0 2.0 3.0 4.0 5.0 6.0 7.0 8.0\n")
+    cf = sc_amd.Cfmtx.read(str(p))
+    plan = sc_amd.Plan(cf, sc_amd.PLAN_CHUNKED)
+    assert not plan.describe(32).startswith("chunk_kernel")
+    B = sc_amd.synth_dense(8 * 32, 5).reshape(8, 32)
+    C = plan.spmm(torch.from_numpy(B).to(DEV)).cpu().numpy()
+    A = np.zeros((4, 8))
+    A[:, 5] = [1, 2, 3, 4]
+    A[:, 1] = [5, 6, 7, 8]
+    assert np.allclose(C, A @ B.astype(np.float64), rtol=1e-6, atol=1e-6)
+
+
+def test_chunk_kernel_generated_unit():
+    # a unit from the reference-compatible generator CLI (km 3, kn 1) runs
+    # through the chunk kernel on a chunked plan
+    unit = sc_amd.GeneratedUnit(os.path.join(os.path.dirname(sc_amd.LIB_PATH), "units",
+                                             "libsc_unit_spmm_km3_kn1.so"), "spmm_km3_kn1")
+    A, B = synth_case(600, 1500, 0.1, 64, seed=0x5EED0000 + 9700)
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 3, 1), sc_amd.PLAN_CHUNKED)
+    C = plan.spmm_generated(unit, torch.from_numpy(B).to(DEV))
+    torch.cuda.synchronize()
+    assert oracle_check(A, B, C.cpu().numpy())[0] <= REL_TOL
