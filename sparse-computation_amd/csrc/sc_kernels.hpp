@@ -193,6 +193,7 @@ __device__ __forceinline__ void store_c(float *dst, const float (&v)[V], int acc
 // loads into load-wait-store round trips.
 __device__ __forceinline__ void keep(float &x) { asm volatile("" : "+v"(x)); }
 __device__ __forceinline__ void keep(int &x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void keep(float2 &x) { asm volatile("" : "+v"(x.x), "+v"(x.y)); }
 __device__ __forceinline__ void keep(float4 &x) {
   asm volatile("" : "+v"(x.x), "+v"(x.y), "+v"(x.z), "+v"(x.w));
 }
@@ -480,6 +481,180 @@ inline ChunkGeometry chunk_geometry(const DevView &v, int N) {
   c.grid = (unsigned)(8 * ((c.ngroups + 7) / 8) * c.nchunks);
   c.use = true;
   return c;
+}
+
+// ---------------------------------------------------------------------------
+// Small-N path (N = 1, 2 or 4, one lane per slot, 64 slots per wave step).
+// At these widths a panel is latency-bound: its pattern segments run one
+// after another in a wave, and each would wait on its own B gather from L2.
+// So the workgroup first stages the panel's values in LDS and gathers
+// B[col(slot), 0..N) of every slot of the panel into LDS, all loads
+// independent and in flight together; the pattern bodies then read only LDS
+// (GatherArgs maps a slot number to its position in the gathered rows, so
+// the generated bodies are used unchanged).
+// ---------------------------------------------------------------------------
+struct GatherArgs {
+  struct Pos {
+    int base;
+    __device__ __forceinline__ int operator[](int j) const { return j - base; }
+  };
+  Pos cols;                        // slot number -> position in the gathered rows
+  const float *__restrict__ vals;  // LDS, indexed with value numbers of the plan
+  const float *gb;                 // LDS, V floats (= N) per position
+  int lo, hi;                      // slot range [lo, hi) of this wave in the segment
+  int sb, vb;                      // first slot / first value of the segment
+  int s, S;                        // slot sub-lane (the lane) and sub-lanes (64)
+};
+
+template <int V>
+__device__ __forceinline__ void load_b(float (&b)[V], const GatherArgs &a, int pos) {
+  const float *p = a.gb + pos * V;
+  if constexpr (V == 4) {
+    const float4 t = *reinterpret_cast<const float4 *>(p);
+    b[0] = t.x;
+    b[1] = t.y;
+    b[2] = t.z;
+    b[3] = t.w;
+  } else if constexpr (V == 2) {
+    const float2 t = *reinterpret_cast<const float2 *>(p);
+    b[0] = t.x;
+    b[1] = t.y;
+  } else {
+    b[0] = *p;
+  }
+}
+
+template <int V>
+struct VecOf;
+template <>
+struct VecOf<1> {
+  using T = float;
+};
+template <>
+struct VecOf<2> {
+  using T = float2;
+};
+template <>
+struct VecOf<4> {
+  using T = float4;
+};
+
+// B (K x V, row-major, V == N) rows of the n slots starting at cols[0] ->
+// dst[i], UNR independent column loads and then UNR row loads in flight.
+template <int V, int UNR>
+__device__ __forceinline__ void gather_rows(typename VecOf<V>::T *dst, const int *__restrict__ cols,
+                                            const typename VecOf<V>::T *__restrict__ Bv, int n) {
+  using T = typename VecOf<V>::T;
+  const int step = blockDim.x;
+  for (int base = threadIdx.x; base < n; base += step * UNR) {
+    int c[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) c[u] = __builtin_nontemporal_load(&cols[min(base + u * step, n - 1)]);
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) keep(c[u]);
+    T r[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) r[u] = Bv[c[u]];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) keep(r[u]);
+#pragma unroll
+    for (int u = 0; u < UNR; ++u)
+      if (base + u * step < n) dst[base + u * step] = r[u];
+  }
+}
+
+template <int KM, int V, class D>
+__global__ void __launch_bounds__(1024)
+    gather_kernel(const int4 *__restrict__ seg, const int *__restrict__ panel_seg,
+                  const int *__restrict__ panel_slot, const int *__restrict__ panel_val,
+                  const int *__restrict__ cols, const float *__restrict__ vals,
+                  const float *__restrict__ B, float *__restrict__ C, int M, int accumulate, int pack,
+                  int stage_vals) {
+  extern __shared__ float smem[];
+  const int panel = blockIdx.x;
+  const int W = blockDim.x >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int p0 = panel_slot[panel];
+  const int p1 = panel_slot[panel + 1];
+  const int npk = (p1 - p0 + pack - 1) / pack;
+  const int per = ((npk + W - 1) / W) * pack;
+  const int a0 = p0 + w * per;
+  const int a1 = min(p1, a0 + per);
+  const int sg0 = panel_seg[panel];
+  const int sg1 = panel_seg[panel + 1];
+  const int q0 = panel_val[panel];
+  const int q1 = panel_val[panel + 1];
+  const int row0 = panel * KM;
+  float *lv = smem;
+  float *gb = smem + stage_vals;
+  stage_copy<8>(lv, vals + q0, q1 - q0);
+  gather_rows<V, 8>(reinterpret_cast<typename VecOf<V>::T *>(gb), cols + p0,
+                    reinterpret_cast<const typename VecOf<V>::T *>(B), p1 - p0);
+  __syncthreads();
+
+  GatherArgs args;
+  args.cols.base = p0;
+  args.vals = lv - q0;
+  args.gb = gb;
+  args.s = lane;
+  args.S = 64;
+  float acc[KM][V];
+#pragma unroll
+  for (int r = 0; r < KM; ++r)
+#pragma unroll
+    for (int e = 0; e < V; ++e) acc[r][e] = 0.f;
+  for (int si = sg0; si < sg1; ++si) {
+    const int4 sd = seg[si];
+    const int lo = max(sd.y, a0);
+    const int hi = min(sd.y + sd.z, a1);
+    if (lo < hi) {
+      args.lo = lo;
+      args.hi = hi;
+      args.sb = sd.y;
+      args.vb = sd.w;
+      D::template run<KM, V>(sd.x, acc, args);
+    }
+  }
+  reduce_slot_lanes<KM, V>(acc, 1);
+  if (W == 1) {
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < KM; ++r)
+        if (row0 + r < M) store_c<V>(C + (size_t)(row0 + r) * V, acc[r], accumulate);
+    }
+  } else {
+    float *red = smem;
+    __syncthreads();  // every wave is done with the staged data
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < KM; ++r)
+#pragma unroll
+        for (int e = 0; e < V; ++e) red[(w * KM + r) * V + e] = acc[r][e];
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < KM * V; t += blockDim.x) {
+      const int r = t / V;
+      const int e = t - r * V;
+      float sum = 0.f;
+      for (int ww = 0; ww < W; ++ww) sum += red[(ww * KM + r) * V + e];
+      const int row = row0 + r;
+      if (row < M) {
+        float *dst = C + (size_t)row * V + e;
+        *dst = accumulate ? *dst + sum : sum;
+      }
+    }
+  }
+}
+
+// LDS bytes of the small-N path for a plan, 0 if it does not apply.
+inline size_t gather_lds(int N, int W, int km, int max_pslots, int max_pvals) {
+  if (!(N == 1 || N == 2 || N == 4) || max_pslots < 0) return 0;
+  const size_t sv = (size_t)(max_pvals + 3) / 4 * 4;
+  const size_t st = (sv + (size_t)max_pslots * N) * sizeof(float);
+  const size_t red = (size_t)W * km * N * sizeof(float);
+  const size_t lds = std::max(st, red);
+  return lds <= 64 * 1024 ? std::max<size_t>(lds, 16) : 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -946,6 +1121,17 @@ hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int 
       else SC_WIDE(1, false);
     }
 #undef SC_WIDE
+    return hipGetLastError();
+  }
+  if (const size_t glds = gather_lds(N, W, KM, v.max_pslots, v.max_pvals)) {
+    const int sv = (v.max_pvals + 3) / 4 * 4;
+#define SC_GATHER(VV)                                                                                   \
+  hipLaunchKernelGGL((gather_kernel<KM, VV, D>), grid, block, glds, stream, v.seg, v.panel_seg,             \
+                     v.panel_slot, v.panel_val, v.cols, v.vals, B, C, v.M, accumulate, pack, sv)
+    if (N == 4) SC_GATHER(4);
+    else if (N == 2) SC_GATHER(2);
+    else SC_GATHER(1);
+#undef SC_GATHER
     return hipGetLastError();
   }
 #define SC_NARROW(VV, ST)                                                                          \

@@ -349,15 +349,18 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
 }
 
 // Waves per panel: enough waves in the grid to cover the 256 CUs several
-// times, but no wave with less than ~2 steps of S slots, and the LDS of the
-// cross-wave reduction within 64 KiB.
+// times, but no wave with less than ~2 steps of S slots unless the panel has
+// many pattern segments (a wave runs its segments one after another, each a
+// full memory round trip, so short segments are spread over more waves), and
+// the LDS of the cross-wave reduction within 64 KiB.
 int auto_waves(const sc_plan *p, int N) {
   if (p->npanels == 0) return 1;
   const sc::Geometry g1 = sc::geometry(p->km, N, 1, p->K, p->view.max_pslots, p->view.max_pvals);
   const int S = 64 / g1.L;
   const double avg = (double)p->nslots / p->npanels;
+  const double segs = (double)p->nsegs / p->npanels;
   int w_occ = (int)std::max<int64_t>(1, 4096 / std::max(1, p->npanels));
-  int w_work = (int)std::max(1.0, avg / (2.0 * S));
+  int w_work = (int)std::max(1.0, std::max(avg / (2.0 * S), segs / 2.0));
   int w = std::min(std::min(w_occ, w_work), 16);
   while (w > 1 && sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals).lds > 65536) --w;
   return std::max(w, 1);
@@ -470,9 +473,14 @@ int sc_plan_describe(const sc_plan *p, int32_t N, char *buf, size_t buflen) {
     } else {
       const int w = auto_waves(p, N);
       const sc::Geometry g = sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals);
-      d = std::string(g.wide ? "wide_kernel" : "panel_kernel") + " km=" + std::to_string(p->km) + " V=" +
-          std::to_string(g.V) + (g.wide ? "" : " L=" + std::to_string(g.L)) + " stage=" +
-          std::to_string(g.stage ? 1 : 0) + " waves=" + std::to_string(w) + " grid=" + std::to_string(p->npanels);
+      if (!g.wide && sc::gather_lds(N, w, p->km, p->view.max_pslots, p->view.max_pvals)) {
+        d = "gather_kernel km=" + std::to_string(p->km) + " V=" + std::to_string(N) + " waves=" +
+            std::to_string(w) + " grid=" + std::to_string(p->npanels);
+      } else {
+        d = std::string(g.wide ? "wide_kernel" : "panel_kernel") + " km=" + std::to_string(p->km) + " V=" +
+            std::to_string(g.V) + (g.wide ? "" : " L=" + std::to_string(g.L)) + " stage=" +
+            std::to_string(g.stage ? 1 : 0) + " waves=" + std::to_string(w) + " grid=" + std::to_string(p->npanels);
+      }
     }
     if (d.size() + 1 > buflen) throw sc::Error{SC_ERR_ARG, "buffer too small"};
     std::memcpy(buf, d.c_str(), d.size() + 1);

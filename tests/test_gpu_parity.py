@@ -257,3 +257,32 @@ def test_chunk_kernel_generated_unit():
     C = plan.spmm_generated(unit, torch.from_numpy(B).to(DEV))
     torch.cuda.synchronize()
     assert oracle_check(A, B, C.cpu().numpy())[0] <= REL_TOL
+
+
+@pytest.mark.parametrize("n", [1, 2, 4])
+@pytest.mark.parametrize("waves", [0, 1, 3, 8, 16])
+def test_small_n_gather_kernel(n, waves):
+    # N = 1, 2, 4: B rows of the panel gathered into LDS before the pattern
+    # bodies run; ragged M, several waves per panel, accumulate
+    A, B = synth_case(515, 700, 0.15, n, seed=0x5EED0000 + 9800 + n * 20 + waves)
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 2))
+    assert plan.describe(n).startswith("gather_kernel")
+    C = run_spmm(A, B, 4, 2, waves=waves)
+    assert oracle_check(A, B, C)[0] <= REL_TOL
+    C0 = sc_amd.synth_dense(515 * n, 19).reshape(515, n)
+    Cacc = run_spmm(A, B, 4, 2, waves=waves, accumulate=C0)
+    ip, ix, ax = csr_f32(A)
+    c64, cab = O.spmm_f64(515, n, ip, ix, ax, B)
+    assert O.max_rel_err(Cacc - C0.astype(np.float64), c64, cab + np.abs(C0)) <= REL_TOL
+
+
+@pytest.mark.parametrize("n", [2, 4])
+def test_small_n_gather_kernel_generated_pack_unit(n):
+    # a kn = 2 unit from the generator CLI: its bodies step two slots at a time
+    unit = sc_amd.GeneratedUnit(os.path.join(os.path.dirname(sc_amd.LIB_PATH), "units",
+                                             "libsc_unit_spmm_km4_kn2.so"), "spmm_km4_kn2")
+    A, B = synth_case(256, 300, 0.2, n, seed=0x5EED0000 + 9900 + n)
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 2))
+    C = plan.spmm_generated(unit, torch.from_numpy(B).to(DEV))
+    torch.cuda.synchronize()
+    assert oracle_check(A, B, C.cpu().numpy())[0] <= REL_TOL
