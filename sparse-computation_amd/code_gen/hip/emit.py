@@ -93,11 +93,10 @@ def _wide_step(rows, pop, slots, indent, loader="sc::load_row"):
 
 def emit_wide_body(km: int, bits: str, pid: int, kn: int, unroll_slots: int = 8) -> str:
     """Wide-path body: the whole wave shares each slot; full batches of
-    `unroll_slots` (a multiple of kn) B-row loads in flight, then one
-    predicated batch for the remainder of the wave's range, so the tail of a
-    segment costs one round trip instead of one per pack.  Its loads are
-    guarded by wave-uniform branches (no load past the end); skipped slots
-    keep zero rows and zero values."""
+    `unroll_slots` (a multiple of kn) B-row loads in flight, then the
+    remainder of the wave's range in power-of-two batches (4, 2, 1 packs for
+    8 slots), so a segment tail costs at most three round trips instead of
+    one per pack, with no loads or FMAs spent on slots past the end."""
     rows = _rows(bits)
     pop = len(rows)
     U = kn * max(1, -(-unroll_slots // kn))
@@ -110,20 +109,18 @@ def emit_wide_body(km: int, bits: str, pid: int, kn: int, unroll_slots: int = 8)
            f"  for (; j + {U} <= a.hi; j += {U}) {{"]
     out += _wide_step(rows, pop, U, "    ")
     out.append("  }")
-    out.append("  if (j < a.hi) {")
-    out.append("    const int last = a.hi - 1 - j;  // last valid offset in this batch (< U - 1)")
-    out.append(f"    const float *vp = a.vals + a.vb + (j - a.sb) * {pop};")
-    for q in range(U):
-        out.append(f"    float b{q}[V] = {{}};")
-    for q in range(U):
-        out.append(f"    if ({q} <= last) sc::load_row<V>(b{q}, a, a.cols[j + {q}]);")
-    for q in range(U):
-        for k in range(pop):
-            out.append(f"    const float v{q}_{k} = {q} <= last ? vp[{q * pop + k}] : 0.0f;")
-    for q in range(U):
-        for k, r in enumerate(rows):
-            out.append(f"    sc::fma_row<V>(acc[{r}], v{q}_{k}, b{q});")
-    out.append("  }")
+    # the remainder (< U slots) in power-of-two batches: at most log2(U/kn)+1
+    # round trips and no wasted loads or FMAs
+    packs = U // kn
+    t = 1
+    while t * 2 < packs:
+        t *= 2
+    while t >= 1:
+        out.append(f"  if (j + {t * kn} <= a.hi) {{")
+        out += _wide_step(rows, pop, t * kn, "    ")
+        out.append(f"    j += {t * kn};")
+        out.append("  }")
+        t //= 2
     out.append("}")
     return "\n".join(out)
 

@@ -50,10 +50,14 @@ class Plan:
         h = C.c_void_p()
         check(lib().sc_plan_create(cf._h, flags, C.byref(h)))
         self._h = h
+        self._free = lib().sc_plan_destroy
 
     def __del__(self):
-        if getattr(self, "_h", None) and self._h.value:
-            lib().sc_plan_destroy(self._h)
+        # the free function is bound at creation: at interpreter exit this
+        # module's globals may already be gone
+        free = getattr(self, "_free", None)
+        if free is not None and getattr(self, "_h", None) and self._h.value:
+            free(self._h)
             self._h = C.c_void_p(None)
 
     def info(self) -> dict:

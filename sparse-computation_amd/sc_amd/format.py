@@ -26,10 +26,14 @@ class Csr:
 
     def __init__(self, handle):
         self._h = C.c_void_p(handle) if not isinstance(handle, C.c_void_p) else handle
+        self._free = lib().sc_csr_free
 
     def __del__(self):
-        if getattr(self, "_h", None) and self._h.value:
-            lib().sc_csr_free(self._h)
+        # the free function is bound at creation: at interpreter exit this
+        # module's globals may already be gone
+        free = getattr(self, "_free", None)
+        if free is not None and getattr(self, "_h", None) and self._h.value:
+            free(self._h)
             self._h = C.c_void_p(None)
 
     @classmethod
@@ -98,10 +102,14 @@ class Cfmtx:
 
     def __init__(self, handle):
         self._h = C.c_void_p(handle) if not isinstance(handle, C.c_void_p) else handle
+        self._free = lib().sc_cfmtx_free
 
     def __del__(self):
-        if getattr(self, "_h", None) and self._h.value:
-            lib().sc_cfmtx_free(self._h)
+        # the free function is bound at creation: at interpreter exit this
+        # module's globals may already be gone
+        free = getattr(self, "_free", None)
+        if free is not None and getattr(self, "_h", None) and self._h.value:
+            free(self._h)
             self._h = C.c_void_p(None)
 
     @classmethod

@@ -75,13 +75,17 @@ class Vendor:
         h = vp()
         _check(vlib().sc_vendor_create(csr._h, kind, N, alg, C.byref(h)))
         self._csr = csr  # keeps the host matrix alive while the handle exists
+        self._destroy = vlib().sc_vendor_destroy
         self.handle = h
         self._bound = None
 
     def __del__(self):
+        # the destroy function is bound at creation: at interpreter exit this
+        # module's globals may already be gone
         h = getattr(self, "handle", None)
-        if h and _v is not None:
-            _v.sc_vendor_destroy(h)
+        destroy = getattr(self, "_destroy", None)
+        if h and destroy is not None:
+            destroy(h)
             self.handle = None
 
     @property
