@@ -161,12 +161,93 @@ def emit_tile_body(km: int, bits: str, pid: int, unroll_slots: int = 8) -> str:
     return "\n".join(out)
 
 
+# ---------------------------------------------------------------------------
+# Pop-count style (the reference's "nnz based" time-analysis variant,
+# code_gen/spmm/spmm_time_analysis.py:73-205): one body per number of rows in
+# the pattern instead of one per pattern; the rows a slot feeds are read from
+# the segment's mask at run time (wave-uniform flags and value ranks), so the
+# unit is smaller and every FMA row sits behind a uniform branch.  Used by
+# main_time_analysis.py to compare the two code-generation styles.
+# ---------------------------------------------------------------------------
+def _mask_rows(km, indent):
+    out = []
+    for r in range(km):
+        out.append(f"{indent}const bool h{r} = (mask & {1 << r}u) != 0;")
+        out.append(f"{indent}const int k{r} = __builtin_popcount(mask & {(1 << r) - 1}u);")
+    return out
+
+
+def _generic_fmas(km, pop, q, indent, value):
+    return [f"{indent}if (h{r}) sc::fma_row<V>(acc[{r}], {value(q, r)}, b{q});" for r in range(km)]
+
+
+def _generic_step(km, pop, slots, indent, loader):
+    out = [f"{indent}const float *vp = a.vals + a.vb + (j - a.sb) * {pop};"]
+    for q in range(slots):
+        out.append(f"{indent}float b{q}[V];")
+        out.append(f"{indent}{loader}<V>(b{q}, a, a.cols[j + {q}]);")
+    for q in range(slots):
+        out += _generic_fmas(km, pop, q, indent, lambda q_, r: f"vp[{q_ * pop} + k{r}]")
+    return out
+
+
+def emit_pop_bodies(km: int, pop: int, kn: int, unroll: int, unroll_slots: int = 8) -> str:
+    head = f"(float (&acc)[{km}][V], const A &a, unsigned mask)"
+    out = [f"// pop-count bodies: {pop} row(s) per slot, rows from the mask"]
+    # lanes over slots
+    out.append("template <int V, class A>")
+    out.append(f"__device__ __forceinline__ void pop{pop}_narrow{head} {{")
+    out += _mask_rows(km, "  ")
+    if unroll > 1:
+        out.append(f"#pragma unroll {unroll}")
+    out.append(f"  for (int j = a.lo + a.s * {kn}; j < a.hi; j += a.S * {kn}) {{")
+    out += _generic_step(km, pop, kn, "    ", "sc::load_b")
+    out.append("  }")
+    out.append("}")
+    # wave-wide slots
+    U = kn * max(1, -(-unroll_slots // kn))
+    out.append("template <int V, class A>")
+    out.append(f"__device__ __forceinline__ void pop{pop}_wide{head} {{")
+    out += _mask_rows(km, "  ")
+    out.append("  int j = a.lo;")
+    out.append(f"  for (; j + {U} <= a.hi; j += {U}) {{")
+    out += _generic_step(km, pop, U, "    ", "sc::load_row")
+    out.append("  }")
+    packs = U // kn
+    t = 1
+    while t * 2 < packs:
+        t *= 2
+    while t >= 1:
+        out.append(f"  if (j + {t * kn} <= a.hi) {{")
+        out += _generic_step(km, pop, t * kn, "    ", "sc::load_row")
+        out.append(f"    j += {t * kn};")
+        out.append("  }")
+        t //= 2
+    out.append("}")
+    # LDS tile (predicated batches)
+    out.append("template <int V, class A>")
+    out.append(f"__device__ __forceinline__ void pop{pop}_tile{head} {{")
+    out += _mask_rows(km, "  ")
+    out.append(f"  for (int j = a.lo; j < a.hi; j += {unroll_slots}) {{")
+    out.append("    const int last = a.hi - 1 - j;")
+    out.append(f"    const float *vp = a.vals + a.vb + (j - a.sb) * {pop};")
+    for q in range(unroll_slots):
+        out.append(f"    float b{q}[V];")
+        out.append(f"    sc::load_tile<V>(b{q}, a, a.cols[j + min({q}, last)]);")
+    for q in range(unroll_slots):
+        out += _generic_fmas(km, pop, q, "    ",
+                             lambda q_, r: f"({q_} <= last ? vp[{q_ * pop} + k{r}] : 0.0f)")
+    out.append("  }")
+    out.append("}")
+    return "\n".join(out)
+
+
 def sanitize(name: str) -> str:
     return re.sub(r"[^0-9A-Za-z_]", "_", name)
 
 
 def emit_unit(name: str, km: int, patterns, kn: int = 1, waves: int = 0, variant: int = 0,
-              unroll: int = 0, origin: str = "", alias: bool = False) -> str:
+              unroll: int = 0, origin: str = "", alias: bool = False, style: str = "pattern") -> str:
     """Return the text of one generated translation unit.
 
     ``patterns``: iterable of (bit string, id) in dictionary order.  Patterns
@@ -175,7 +256,11 @@ def emit_unit(name: str, km: int, patterns, kn: int = 1, waves: int = 0, variant
     ``variant``: 0 = any N, otherwise the only N the launcher accepts.
     ``alias``: also export the unit as sc_gen_unit_record / sc_gen_unit_launch
     (the fixed names the demo drivers link against).
+    ``style``: "pattern" (one straight-line body per pattern) or "popcount"
+    (one body per number of rows, rows read from the mask at run time).
     """
+    if style not in ("pattern", "popcount"):
+        raise ValueError("style must be 'pattern' or 'popcount'")
     if km < 1 or km > 20:
         raise ValueError("km must be in 1..20")
     if kn < 1:
@@ -201,6 +286,35 @@ def emit_unit(name: str, km: int, patterns, kn: int = 1, waves: int = 0, variant
     out.append("")
     out.append(f"namespace sc_gen_{name} {{")
     out.append("")
+    if style == "popcount":
+        pops = sorted({bits.count("1") for bits, _ in usable})
+        for p in pops:
+            out.append(emit_pop_bodies(km, p, kn, unroll))
+            out.append("")
+        out.append("struct dispatch {")
+        for kind, args in (("run_tile", "sc::TileArgs"), ("run_wide", "sc::WideArgs"), ("run", None)):
+            body = {"run_tile": "tile", "run_wide": "wide", "run": "narrow"}[kind]
+            if args:
+                out.append("  template <int KM, int V>")
+                out.append(f"  __device__ __forceinline__ static void {kind}(int mask, float (&acc)[KM][V], "
+                           f"const {args} &a) {{")
+            else:
+                out.append("  template <int KM, int V, class A>")
+                out.append(f"  __device__ __forceinline__ static void {kind}(int mask, float (&acc)[KM][V], "
+                           "const A &a) {")
+            out.append(f"    static_assert(KM == {km}, \"dispatcher generated for km={km}\");")
+            out.append("    switch (__builtin_popcount((unsigned)mask)) {")
+            for p in pops:
+                targs = "V" if args else "V, A"
+                out.append(f"      case {p}: pop{p}_{body}<{targs}>(acc, a, (unsigned)mask); break;")
+            out.append("      default: break;")
+            out.append("    }")
+            out.append("  }")
+        out.append("};")
+        out.append("")
+        out.append(f"}}  // namespace sc_gen_{name}")
+        out.append("")
+        return _emit_exports(out, name, km, kn, waves, variant, usable, alias)
     for bits, pid in usable:
         out.append(emit_body(km, bits, pid, kn, unroll))
         out.append("")
@@ -241,6 +355,11 @@ def emit_unit(name: str, km: int, patterns, kn: int = 1, waves: int = 0, variant
     out.append("")
     out.append(f"}}  // namespace sc_gen_{name}")
     out.append("")
+    return _emit_exports(out, name, km, kn, waves, variant, usable, alias)
+
+
+def _emit_exports(out, name, km, kn, waves, variant, usable, alias):
+    """The unit's extern "C" record, masks, launcher and optional alias."""
     masks = ", ".join(f"{_mask(b)}u" for b, _ in usable) or "0u"
     out.append(f'extern "C" __attribute__((visibility("default"))) const uint32_t '
                f"sc_gen_{name}_masks[] = {{{masks}}};")

@@ -134,3 +134,35 @@ def test_run_script_builds_the_demo(tmp_path):
         assert a.read() == b.read()
     assert os.access(os.path.join(ROOT, "sparse-computation_amd", "build",
                                   "spmm_small_b_col_demo_gpu"), os.X_OK)
+
+
+def test_time_analysis_generator_styles(tmp_path):
+    # main_time_analysis.py <out> <m> <n> <compact>: pop-count bodies (compact 1)
+    # or one body per pattern (compact 0), each with a standalone driver
+    sys.path.insert(0, CG)
+    import main_time_analysis as ta
+    pop = tmp_path / "pop.hip"
+    pat = tmp_path / "pat.hip"
+    run(os.path.join(CG, "main_time_analysis.py"), str(pop), "4", "1", "1")
+    run(os.path.join(CG, "main_time_analysis.py"), str(pat), "4", "1", "0")
+    tp, tt = pop.read_text(), pat.read_text()
+    for p in (1, 2, 3, 4):
+        assert f"void pop{p}_wide(" in tp and f"void pop{p}_narrow(" in tp
+    assert "pattern_1111" not in tp and "switch (__builtin_popcount((unsigned)mask))" in tp
+    assert len(_cases(tt)) == 15 and "void wide_1011(" in tt
+    for t, style in ((tp, "popcount"), (tt, "pattern")):
+        assert "int main(int argc, char **argv)" in t and f"sc_gen_ta_{style}_km4_kn1_launch" in t
+    assert ta.unit_name(4, 1, True) == "ta_popcount_km4_kn1"
+
+
+@pytest.mark.skipif(not os.path.exists("/opt/rocm/bin/hipcc"), reason="hipcc not installed")
+def test_time_analysis_resource_report(tmp_path):
+    out = run(os.path.join(CG, "main_time_analysis.py"), str(tmp_path / "p.hip"), "3", "1", "1",
+              "--report").stdout
+    lines = out.splitlines()
+    i = lines.index("kernel,code_bytes,vgprs,sgprs,scratch_bytes_per_lane,occupancy_waves_per_simd")
+    rows = [l.split(",") for l in lines[i + 1:]]
+    kernels = {r[0] for r in rows}
+    assert "wide_kernel(km=3 V=2 stage)" in kernels and "gather_kernel(km=3 V=1)" in kernels
+    for r in rows:
+        assert int(r[2]) > 0 and int(r[4]) == 0  # VGPRs used, nothing spilled to scratch
