@@ -117,8 +117,9 @@ void sc_cfmtx_free(sc_cfmtx *cf);
 /* Plan flags */
 #define SC_PLAN_DROP_PADDING 1 /* omit the zero-valued padding slots on the device */
 #define SC_PLAN_TILED 2        /* also build the split-K LDS-tiled copy (opt-in)    */
-#define SC_PLAN_CHUNKED 4      /* build the column splits of the chunk kernel (B
-                                  column chunks resident in LDS, N % 32 == 0)      */
+#define SC_PLAN_CHUNKED 4      /* build the K-block-major copy of the chunk kernel
+                                  (B column chunks resident in LDS, N % 32 == 0)   */
+#define SC_PLAN_F16_VALUES 8   /* also keep a binary16 copy of the values (sc_spmm_f16) */
 
 /* allocateAndCopyMixedFormat (example_cuda/spmm_demo_gpu_utils.h:207-245) and
  * the constructors of the generated classes SpMMMixePatternGeneralCacheLess /
@@ -147,6 +148,16 @@ int sc_spmm(const sc_plan *plan, const float *dB, float *dC, int32_t N, int32_t 
             int32_t waves_per_panel, void *hip_stream);
 /* y = A*x (N = 1). */
 int sc_spmv(const sc_plan *plan, const float *dx, float *dy, int32_t flags, void *hip_stream);
+/* The binary16 small-B path: C = A*B with A's values (the plan's binary16
+ * copy: create the plan with SC_PLAN_F16_VALUES), B (K x N) and C (M x N) in
+ * IEEE binary16, N = 1, 2 or 4, fp32 accumulation, C rounded once to nearest
+ * even.  Replaces the reference's fp16 small-B kernels
+ * (SpmvComplexPatternDecomposeByRowSeperatedHalf, PatternWith{pop}NNZByRowPanelFullHALF:
+ * example_cuda/spmm_small_b_col_demo_gpu_utils.h:2987-4910, generator
+ * code_gen/spmm_small_b_col/spmm_small_b_col_format_code_generator.py:326-435),
+ * which accumulate in binary16. */
+int sc_spmm_f16(const sc_plan *plan, const void *dB, void *dC, int32_t N, int32_t flags,
+                int32_t waves_per_panel, void *hip_stream);
 void sc_plan_destroy(sc_plan *plan);
 
 /* ------------------------------------------------------- generated kernels */

@@ -380,6 +380,20 @@ def _emit_exports(out, name, km, kn, waves, variant, usable, alias):
                f"waves, {kn}, stream);")
     out.append("}")
     out.append("")
+    # binary16 values / B / C (N = 1, 2, 4; the plan holds a binary16 copy of its values)
+    out.append(f'extern "C" __attribute__((visibility("default"))) hipError_t '
+               f"sc_gen_{name}_launch_f16(const sc::DevView *v, const void *B, void *C, int N,")
+    out.append("                                             int accumulate, int waves, "
+               "hipStream_t stream) {")
+    if variant:
+        out.append(f"  if (N != {variant}) return hipErrorInvalidValue;")
+    if waves:
+        out.append(f"  if (waves <= 0) waves = {waves};")
+    out.append("  if (waves <= 0) waves = 1;")
+    out.append(f"  return sc::launch_panels_f16<{km}, sc_gen_{name}::dispatch>(*v, B, C, N, accumulate, "
+               f"waves, {kn}, stream);")
+    out.append("}")
+    out.append("")
     if alias:
         out.append('extern "C" __attribute__((visibility("default"))) const sc_gen_record *'
                    f"sc_gen_unit_record = &sc_gen_{name}_record;")

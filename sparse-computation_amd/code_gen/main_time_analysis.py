@@ -193,7 +193,13 @@ def short_kernel(mangled):
         m1 = re.match(r"_ZN2sc\d+(\w+?)I", mangled)
         return m1.group(1) if m1 else mangled[:60]
     name, km, v, flag = m.groups()
-    return f"{name}(km={km} V={v}" + (f" {'stage' if flag == '1' else 'nostage'}" if flag else "") + ")"
+    if flag and name == "gather_kernel":
+        tag = " f16" if flag == "1" else " f32"  # binary16 values / B / C
+    elif flag:
+        tag = " stage" if flag == "1" else " nostage"
+    else:
+        tag = ""
+    return f"{name}(km={km} V={v}{tag})"
 
 
 def main(argv=None):

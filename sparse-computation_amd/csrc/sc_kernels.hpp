@@ -27,6 +27,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "sc_api.h"
 
@@ -69,6 +70,7 @@ struct DevView {
   long long work_floats;  // its size in floats
   int kblock_kind;        // what the K-block-major copy was built for: 0 none,
                           // 1 the split-K tiled kernel, 2 the chunk kernel
+  const _Float16 *vals16; // binary16 copy of vals (SC_PLAN_F16_VALUES), or null
 };
 
 // Chunk kernel: columns of B per chunk, B rows per K block (LDS tile), and
@@ -539,12 +541,54 @@ struct VecOf<4> {
   using T = float4;
 };
 
-// B (K x V, row-major, V == N) rows of the n slots starting at cols[0] ->
-// dst[i], UNR independent column loads and then UNR row loads in flight.
-template <int V, int UNR>
+// Rows of V binary16 values, loaded as one 2-, 4- or 8-byte word.
+template <int V>
+struct HalfRowOf;
+template <>
+struct HalfRowOf<1> {
+  using T = unsigned short;
+};
+template <>
+struct HalfRowOf<2> {
+  using T = unsigned int;
+};
+template <>
+struct HalfRowOf<4> {
+  using T = uint2;
+};
+__device__ __forceinline__ void keep(unsigned short &x) {
+  unsigned int t = x;
+  asm volatile("" : "+v"(t));
+  x = (unsigned short)t;
+}
+__device__ __forceinline__ void keep(unsigned int &x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void keep(uint2 &x) { asm volatile("" : "+v"(x.x), "+v"(x.y)); }
+
+__device__ __forceinline__ float half_bits_to_float(unsigned int h16) {
+  return (float)__builtin_bit_cast(_Float16, (unsigned short)h16);
+}
+
+// Row of V binary16 values -> V floats (exact).
+template <int V>
+__device__ __forceinline__ typename VecOf<V>::T widen_row(typename HalfRowOf<V>::T r) {
+  if constexpr (V == 4) {
+    return make_float4(half_bits_to_float(r.x & 0xffffu), half_bits_to_float(r.x >> 16),
+                       half_bits_to_float(r.y & 0xffffu), half_bits_to_float(r.y >> 16));
+  } else if constexpr (V == 2) {
+    return make_float2(half_bits_to_float(r & 0xffffu), half_bits_to_float(r >> 16));
+  } else {
+    return half_bits_to_float(r);
+  }
+}
+
+// B (K x V, row-major, V == N; fp32, or binary16 when HALF) rows of the n
+// slots starting at cols[0] -> dst[i] as fp32, UNR independent column loads
+// and then UNR row loads in flight.
+template <int V, int UNR, bool HALF>
 __device__ __forceinline__ void gather_rows(typename VecOf<V>::T *dst, const int *__restrict__ cols,
-                                            const typename VecOf<V>::T *__restrict__ Bv, int n) {
-  using T = typename VecOf<V>::T;
+                                            const void *__restrict__ B, int n) {
+  using T = typename std::conditional<HALF, typename HalfRowOf<V>::T, typename VecOf<V>::T>::type;
+  const T *Bv = reinterpret_cast<const T *>(B);
   const int step = blockDim.x;
   for (int base = threadIdx.x; base < n; base += step * UNR) {
     int c[UNR];
@@ -559,16 +603,51 @@ __device__ __forceinline__ void gather_rows(typename VecOf<V>::T *dst, const int
     for (int u = 0; u < UNR; ++u) keep(r[u]);
 #pragma unroll
     for (int u = 0; u < UNR; ++u)
-      if (base + u * step < n) dst[base + u * step] = r[u];
+      if (base + u * step < n) {
+        if constexpr (HALF) dst[base + u * step] = widen_row<V>(r[u]);
+        else dst[base + u * step] = r[u];
+      }
   }
 }
 
-template <int KM, int V, class D>
+// n binary16 values (bits) -> fp32 in dst, UNR loads in flight per thread.
+template <int UNR>
+__device__ __forceinline__ void stage_half_values(float *dst, const unsigned short *__restrict__ src, int n) {
+  if (n <= 0) return;
+  const int step = blockDim.x;
+  for (int base = threadIdx.x; base < n; base += step * UNR) {
+    unsigned short r[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) r[u] = src[min(base + u * step, n - 1)];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) keep(r[u]);
+#pragma unroll
+    for (int u = 0; u < UNR; ++u)
+      if (base + u * step < n) dst[base + u * step] = half_bits_to_float(r[u]);
+  }
+}
+
+// C row segment of V values: fp32, or binary16 (rounded to nearest even)
+// when HALF; with accumulate the old value is added in fp32 first.
+template <int V, bool HALF>
+__device__ __forceinline__ void store_row(void *C, size_t off, const float (&v)[V], int accumulate) {
+  if constexpr (HALF) {
+    _Float16 *c = reinterpret_cast<_Float16 *>(C) + off;
+#pragma unroll
+    for (int e = 0; e < V; ++e) c[e] = (_Float16)(accumulate ? (float)c[e] + v[e] : v[e]);
+  } else {
+    store_c<V>(reinterpret_cast<float *>(C) + off, v, accumulate);
+  }
+}
+
+// HALF: values (vals16 of the plan), B and C are binary16; staging widens
+// them to fp32 in LDS, the bodies accumulate in fp32 and C is rounded once.
+template <int KM, int V, bool HALF, class D>
 __global__ void __launch_bounds__(1024)
     gather_kernel(const int4 *__restrict__ seg, const int *__restrict__ panel_seg,
                   const int *__restrict__ panel_slot, const int *__restrict__ panel_val,
-                  const int *__restrict__ cols, const float *__restrict__ vals,
-                  const float *__restrict__ B, float *__restrict__ C, int M, int accumulate, int pack,
+                  const int *__restrict__ cols, const void *__restrict__ vals,
+                  const void *__restrict__ B, void *__restrict__ C, int M, int accumulate, int pack,
                   int stage_vals) {
   extern __shared__ float smem[];
   const int panel = blockIdx.x;
@@ -588,9 +667,11 @@ __global__ void __launch_bounds__(1024)
   const int row0 = panel * KM;
   float *lv = smem;
   float *gb = smem + stage_vals;
-  stage_copy<8>(lv, vals + q0, q1 - q0);
-  gather_rows<V, 8>(reinterpret_cast<typename VecOf<V>::T *>(gb), cols + p0,
-                    reinterpret_cast<const typename VecOf<V>::T *>(B), p1 - p0);
+  if constexpr (HALF)
+    stage_half_values<8>(lv, reinterpret_cast<const unsigned short *>(vals) + q0, q1 - q0);
+  else
+    stage_copy<8>(lv, reinterpret_cast<const float *>(vals) + q0, q1 - q0);
+  gather_rows<V, 8, HALF>(reinterpret_cast<typename VecOf<V>::T *>(gb), cols + p0, B, p1 - p0);
   __syncthreads();
 
   GatherArgs args;
@@ -621,7 +702,7 @@ __global__ void __launch_bounds__(1024)
     if (lane == 0) {
 #pragma unroll
       for (int r = 0; r < KM; ++r)
-        if (row0 + r < M) store_c<V>(C + (size_t)(row0 + r) * V, acc[r], accumulate);
+        if (row0 + r < M) store_row<V, HALF>(C, (size_t)(row0 + r) * V, acc[r], accumulate);
     }
   } else {
     float *red = smem;
@@ -640,8 +721,8 @@ __global__ void __launch_bounds__(1024)
       for (int ww = 0; ww < W; ++ww) sum += red[(ww * KM + r) * V + e];
       const int row = row0 + r;
       if (row < M) {
-        float *dst = C + (size_t)row * V + e;
-        *dst = accumulate ? *dst + sum : sum;
+        const float one[1] = {sum};
+        store_row<1, HALF>(C, (size_t)row * V + e, one, accumulate);
       }
     }
   }
@@ -1126,7 +1207,7 @@ hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int 
   if (const size_t glds = gather_lds(N, W, KM, v.max_pslots, v.max_pvals)) {
     const int sv = (v.max_pvals + 3) / 4 * 4;
 #define SC_GATHER(VV)                                                                                   \
-  hipLaunchKernelGGL((gather_kernel<KM, VV, D>), grid, block, glds, stream, v.seg, v.panel_seg,             \
+  hipLaunchKernelGGL((gather_kernel<KM, VV, false, D>), grid, block, glds, stream, v.seg, v.panel_seg,      \
                      v.panel_slot, v.panel_val, v.cols, v.vals, B, C, v.M, accumulate, pack, sv)
     if (N == 4) SC_GATHER(4);
     else if (N == 2) SC_GATHER(2);
@@ -1148,6 +1229,28 @@ hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int 
     else SC_NARROW(1, false);
   }
 #undef SC_NARROW
+  return hipGetLastError();
+}
+
+// binary16 values, B and C (N = 1, 2 or 4): the small-N gather kernel with
+// fp32 accumulation.  The counterpart of the reference's fp16 small-B bodies
+// (PatternWith{pop}NNZByRowPanelFullHALF), which accumulate in binary16.
+template <int KM, class D>
+hipError_t launch_panels_f16(const DevView &v, const void *B, void *C, int N, int accumulate, int W,
+                             int pack, hipStream_t stream) {
+  if (!v.vals16 || !(N == 1 || N == 2 || N == 4)) return hipErrorInvalidValue;
+  if (v.npanels <= 0) return hipSuccess;
+  const size_t glds = gather_lds(N, W, KM, v.max_pslots, v.max_pvals);
+  if (!glds) return hipErrorInvalidValue;
+  const int sv = (v.max_pvals + 3) / 4 * 4;
+  dim3 grid((unsigned)v.npanels), block((unsigned)(64 * W));
+#define SC_GATHER16(VV)                                                                                 \
+  hipLaunchKernelGGL((gather_kernel<KM, VV, true, D>), grid, block, glds, stream, v.seg, v.panel_seg,       \
+                     v.panel_slot, v.panel_val, v.cols, v.vals16, B, C, v.M, accumulate, pack, sv)
+  if (N == 4) SC_GATHER16(4);
+  else if (N == 2) SC_GATHER16(2);
+  else SC_GATHER16(1);
+#undef SC_GATHER16
   return hipGetLastError();
 }
 

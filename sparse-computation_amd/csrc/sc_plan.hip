@@ -30,7 +30,9 @@ const sc::Cfmtx &sc_cfmtx_ref(const sc_cfmtx *cf);
 #define SC_DECLARE_GEN(k)                                                                        \
   extern "C" const sc_gen_record sc_gen_builtin_km##k##_record;                                  \
   extern "C" hipError_t sc_gen_builtin_km##k##_launch(const sc::DevView *, const float *, float *, \
-                                                      int, int, int, hipStream_t);
+                                                      int, int, int, hipStream_t);               \
+  extern "C" hipError_t sc_gen_builtin_km##k##_launch_f16(const sc::DevView *, const void *, void *, \
+                                                          int, int, int, hipStream_t);
 SC_DECLARE_GEN(1)
 SC_DECLARE_GEN(2)
 SC_DECLARE_GEN(3)
@@ -42,20 +44,20 @@ namespace {
 
 using LaunchFn = hipError_t (*)(const sc::DevView *, const float *, float *, int, int, int, hipStream_t);
 
+using LaunchF16Fn = hipError_t (*)(const sc::DevView *, const void *, void *, int, int, int, hipStream_t);
+
 struct GenEntry {
   const sc_gen_record *rec;
   LaunchFn launch;
+  LaunchF16Fn launch_f16;
 };
 
+#define SC_GEN_ENTRY(k) {&sc_gen_builtin_km##k##_record, sc_gen_builtin_km##k##_launch, sc_gen_builtin_km##k##_launch_f16}
 const GenEntry kBuiltin[] = {
-    {nullptr, nullptr},
-    {&sc_gen_builtin_km1_record, sc_gen_builtin_km1_launch},
-    {&sc_gen_builtin_km2_record, sc_gen_builtin_km2_launch},
-    {&sc_gen_builtin_km3_record, sc_gen_builtin_km3_launch},
-    {&sc_gen_builtin_km4_record, sc_gen_builtin_km4_launch},
-    {&sc_gen_builtin_km5_record, sc_gen_builtin_km5_launch},
-    {&sc_gen_builtin_km6_record, sc_gen_builtin_km6_launch},
+    {nullptr, nullptr, nullptr}, SC_GEN_ENTRY(1), SC_GEN_ENTRY(2), SC_GEN_ENTRY(3),
+    SC_GEN_ENTRY(4),             SC_GEN_ENTRY(5), SC_GEN_ENTRY(6),
 };
+#undef SC_GEN_ENTRY
 constexpr int kMaxBuiltinKm = 6;
 constexpr int kTileRows = 256;           // B rows per K block of the tiled kernel
 constexpr double kTileMinReuse = 3.0;    // slots per staged B row to build the tiled copy
@@ -295,7 +297,14 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   size_t off_kpval = align_up<int>(off_kpslot + kp_slot.size() * sizeof(int32_t));
   size_t off_tcols = align_up<int>(off_kpval + kp_val.size() * sizeof(int32_t));
   size_t off_tvals = align_up<int>(off_tcols + tcols.size() * sizeof(int32_t));
-  size_t total = align_up<int>(off_tvals + tvals.size() * sizeof(float));
+  // binary16 copy of the values (SC_PLAN_F16_VALUES), rounded to nearest even
+  std::vector<_Float16> vals16;
+  if (flags & SC_PLAN_F16_VALUES) {
+    vals16.resize(vals.size());
+    for (size_t i = 0; i < vals.size(); ++i) vals16[i] = (_Float16)vals[i];
+  }
+  size_t off_v16 = align_up<int>(off_tvals + tvals.size() * sizeof(float));
+  size_t total = align_up<int>(off_v16 + vals16.size() * sizeof(_Float16));
   hip_check(hipMalloc(&plan->dmem, total), "hipMalloc(plan)");
   std::vector<unsigned char> host(total, 0);
   std::memcpy(host.data() + off_seg, seg.data(), seg.size() * sizeof(int4));
@@ -310,6 +319,7 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   std::memcpy(host.data() + off_tvals, tvals.data(), tvals.size() * sizeof(float));
   std::memcpy(host.data() + off_cols, cols.data(), cols.size() * sizeof(int32_t));
   std::memcpy(host.data() + off_vals, vals.data(), vals.size() * sizeof(float));
+  std::memcpy(host.data() + off_v16, vals16.data(), vals16.size() * sizeof(_Float16));
   hipError_t e = hipMemcpy(plan->dmem, host.data(), total, hipMemcpyHostToDevice);
   if (e != hipSuccess) {
     (void)hipFree(plan->dmem);
@@ -345,6 +355,7 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   plan->view.work = nullptr;
   plan->view.work_floats = 0;
   plan->view.kblock_kind = kind;
+  plan->view.vals16 = vals16.empty() ? nullptr : (const _Float16 *)(base + off_v16);
   return plan.release();
 }
 
@@ -431,7 +442,7 @@ extern "C" {
 int sc_plan_create(const sc_cfmtx *cf, int32_t flags, sc_plan **out) {
   SC_GUARD([&] {
     if (!cf || !out) throw sc::Error{SC_ERR_ARG, "null argument"};
-    if (flags & ~(SC_PLAN_DROP_PADDING | SC_PLAN_TILED | SC_PLAN_CHUNKED))
+    if (flags & ~(SC_PLAN_DROP_PADDING | SC_PLAN_TILED | SC_PLAN_CHUNKED | SC_PLAN_F16_VALUES))
       throw sc::Error{SC_ERR_ARG, "unknown plan flags"};
     if ((flags & SC_PLAN_TILED) && (flags & SC_PLAN_CHUNKED))
       throw sc::Error{SC_ERR_ARG, "SC_PLAN_TILED and SC_PLAN_CHUNKED are exclusive"};
@@ -509,6 +520,31 @@ int sc_spmv(const sc_plan *plan, const float *dx, float *dy, int32_t flags, void
     if (flags & ~SC_ACCUMULATE) throw sc::Error{SC_ERR_ARG, "unknown flags"};
     if (!plan) throw sc::Error{SC_ERR_ARG, "null plan"};
     launch(plan, plan->gen.rec, (sc_gen_launch_fn)plan->gen.launch, dx, dy, 1, flags, 0, hip_stream);
+  });
+}
+
+int sc_spmm_f16(const sc_plan *plan, const void *dB, void *dC, int32_t N, int32_t flags,
+                int32_t waves_per_panel, void *hip_stream) {
+  SC_GUARD([&] {
+    if (flags & ~SC_ACCUMULATE) throw sc::Error{SC_ERR_ARG, "unknown flags"};
+    if (!plan) throw sc::Error{SC_ERR_ARG, "null plan"};
+    if (!plan->view.vals16)
+      throw sc::Error{SC_ERR_ARG, "plan has no binary16 values (create it with SC_PLAN_F16_VALUES)"};
+    if (!(N == 1 || N == 2 || N == 4))
+      throw sc::Error{SC_ERR_UNSUPPORTED, "the binary16 path takes N = 1, 2 or 4"};
+    if (!dB || !dC) throw sc::Error{SC_ERR_ARG, "null device buffer"};
+    if ((uintptr_t)dB % (2 * N) || (uintptr_t)dC % 2)
+      throw sc::Error{SC_ERR_ARG, "B must be aligned to 2*N bytes and C to 2 bytes"};
+    if (waves_per_panel < 0 || waves_per_panel > 16) throw sc::Error{SC_ERR_ARG, "waves per panel must be 0..16"};
+    int dev = -1;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev != plan->device) throw sc::Error{SC_ERR_ARG, "plan lives on another device than the current one"};
+    int w = waves_per_panel ? waves_per_panel : auto_waves(plan, N);
+    if (!sc::gather_lds(N, w, plan->km, plan->view.max_pslots, plan->view.max_pvals))
+      throw sc::Error{SC_ERR_UNSUPPORTED, "a panel of this plan does not fit the binary16 path's LDS staging"};
+    hip_check(plan->gen.launch_f16(&plan->view, dB, dC, N, (flags & SC_ACCUMULATE) ? 1 : 0, w,
+                                   (hipStream_t)hip_stream),
+              "binary16 pattern kernel launch");
   });
 }
 

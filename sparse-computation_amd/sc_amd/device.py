@@ -12,6 +12,7 @@ from .format import Cfmtx
 PLAN_DROP_PADDING = 1
 PLAN_TILED = 2
 PLAN_CHUNKED = 4
+PLAN_F16_VALUES = 8
 ACCUMULATE = 1
 
 
@@ -111,6 +112,22 @@ class Plan:
                                       C.c_void_p(B.data_ptr()), C.c_void_p(C_out.data_ptr()), N,
                                       ACCUMULATE if accumulate else 0, waves,
                                       _stream_handle(stream)))
+        return C_out
+
+    def spmm_f16(self, B, C_out=None, accumulate=False, waves=0, stream=None):
+        """C = A @ B in binary16 (B: K x N float16 CUDA tensor, N in 1, 2, 4;
+        the plan must be created with PLAN_F16_VALUES).  fp32 accumulation."""
+        info = self.info()
+        N = B.shape[1] if B.dim() == 2 else 1
+        if B.dtype != torch.float16 or not B.is_cuda or not B.is_contiguous() or B.shape[0] != info["n"]:
+            raise ValueError(f"B must be a contiguous ({info['n']}, N) float16 device tensor")
+        if C_out is None:
+            C_out = torch.empty((info["m"], N), dtype=torch.float16, device=B.device)
+        if (C_out.dtype != torch.float16 or not C_out.is_contiguous() or C_out.shape[0] != info["m"]
+                or C_out.numel() != info["m"] * N):
+            raise ValueError(f"C must be a contiguous ({info['m']}, {N}) float16 device tensor")
+        check(lib().sc_spmm_f16(self._h, C.c_void_p(B.data_ptr()), C.c_void_p(C_out.data_ptr()), N,
+                                ACCUMULATE if accumulate else 0, waves, _stream_handle(stream)))
         return C_out
 
     def spmv(self, x, y=None, accumulate=False, stream=None):

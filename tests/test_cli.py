@@ -163,6 +163,6 @@ def test_time_analysis_resource_report(tmp_path):
     i = lines.index("kernel,code_bytes,vgprs,sgprs,scratch_bytes_per_lane,occupancy_waves_per_simd")
     rows = [l.split(",") for l in lines[i + 1:]]
     kernels = {r[0] for r in rows}
-    assert "wide_kernel(km=3 V=2 stage)" in kernels and "gather_kernel(km=3 V=1)" in kernels
+    assert "wide_kernel(km=3 V=2 stage)" in kernels and "gather_kernel(km=3 V=1 f32)" in kernels
     for r in rows:
         assert int(r[2]) > 0 and int(r[4]) == 0  # VGPRs used, nothing spilled to scratch
