@@ -106,8 +106,28 @@ def emit_wide_body(km: int, bits: str, pid: int, kn: int, unroll_slots: int = 8)
            f"__device__ __forceinline__ void {wide_name(bits)}(float (&acc)[{km}][V], "
            "const sc::WideArgs &a) {",
            "  int j = a.lo;",
-           f"  for (; j + {U} <= a.hi; j += {U}) {{"]
-    out += _wide_step(rows, pop, U, "    ")
+           f"  if (j + {U} <= a.hi) {{"]
+    for q in range(U):
+        out.append(f"    int c{q} = a.cols[j + {q}];")
+    out.append("    for (;;) {")
+    for q in range(U):
+        out.append(f"      float b{q}[V];")
+        out.append(f"      sc::load_row<V>(b{q}, a, c{q});")
+    out.append(f"      const float *vp = a.vals + a.vb + (j - a.sb) * {pop};")
+    for q in range(U):
+        for k in range(pop):
+            out.append(f"      const float v{q}_{k} = vp[{q * pop + k}];")
+    out.append(f"      const bool more = j + {2 * U} <= a.hi;")
+    out.append("      if (more) {")
+    for q in range(U):
+        out.append(f"        c{q} = a.cols[j + {U + q}];")
+    out.append("      }")
+    for q in range(U):
+        for k, r in enumerate(rows):
+            out.append(f"      sc::fma_row<V>(acc[{r}], v{q}_{k}, b{q});")
+    out.append(f"      j += {U};")
+    out.append("      if (!more) break;")
+    out.append("    }")
     out.append("  }")
     # the remainder (< U slots) in power-of-two batches: at most log2(U/kn)+1
     # round trips and no wasted loads or FMAs

@@ -71,6 +71,7 @@ struct DevView {
   int kblock_kind;        // what the K-block-major copy was built for: 0 none,
                           // 1 the split-K tiled kernel, 2 the chunk kernel
   const _Float16 *vals16; // binary16 copy of vals (SC_PLAN_F16_VALUES), or null
+  long long a_bytes;      // bytes of the plan's column and value streams
 };
 
 // Chunk kernel: columns of B per chunk, B rows per K block (LDS tile), and
@@ -1103,9 +1104,16 @@ struct Geometry {
 };
 
 constexpr size_t kStageLimit = 64 * 1024;
+// The wide and narrow kernels stage a panel's stream in LDS only when the
+// plan's streams are at least this large: such a plan comes from HBM, where
+// one batched copy per panel beats a load round trip per batch of slots
+// (4096^2 at 10 %, N=128: 31.3 vs 33.6 us).  Smaller plans stay in L2 and run
+// faster unstaged (FFN 2048x512 at 50 %: 11.4 vs 12.7 us; 512^2 at 10 %,
+// N=32: 7.3 vs 7.9 us).
+constexpr long long kStageMinBytes = 8ll << 20;
 
 inline Geometry geometry(int km, int N, int W, long long K = 0, int max_pslots = -1,
-                         int max_pvals = -1) {
+                         int max_pvals = -1, long long a_bytes = -1) {
   Geometry g;
   g.stage = false;
   g.stage_cols = 0;
@@ -1116,7 +1124,7 @@ inline Geometry geometry(int km, int N, int W, long long K = 0, int max_pslots =
     g.L = 64;
     const size_t red = W > 1 ? (size_t)W * km * 64 * wv * sizeof(float) : 0;
     g.lds = red;
-    if (max_pslots >= 0) {
+    if (max_pslots >= 0 && (a_bytes < 0 || a_bytes >= kStageMinBytes)) {
       const int sc = (max_pslots + 3) / 4 * 4;
       const size_t st = ((size_t)sc + (size_t)max_pvals) * 4;
       if (st <= kStageLimit) {
@@ -1134,7 +1142,7 @@ inline Geometry geometry(int km, int N, int W, long long K = 0, int max_pslots =
   while (g.L < groups && g.L < 64) g.L <<= 1;
   const size_t red = W > 1 ? (size_t)W * km * g.L * g.V * sizeof(float) : 0;
   g.lds = red;
-  if (max_pslots >= 0) {
+  if (max_pslots >= 0 && (a_bytes < 0 || a_bytes >= kStageMinBytes)) {
     const int sc = (max_pslots + 3) / 4 * 4;
     const size_t st = ((size_t)sc + (size_t)max_pvals) * 4;
     if (st <= kStageLimit) {
@@ -1185,7 +1193,7 @@ hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int 
       return hipGetLastError();
     }
   }
-  const Geometry g = geometry(KM, N, W, v.K, v.max_pslots, v.max_pvals);
+  const Geometry g = geometry(KM, N, W, v.K, v.max_pslots, v.max_pvals, v.a_bytes);
   dim3 grid((unsigned)v.npanels), block((unsigned)(64 * W));
   if (g.wide) {
 #define SC_WIDE(VV, ST)                                                                           \

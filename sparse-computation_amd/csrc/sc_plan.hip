@@ -355,6 +355,7 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   plan->view.work = nullptr;
   plan->view.work_floats = 0;
   plan->view.kblock_kind = kind;
+  plan->view.a_bytes = 4ll * ((long long)cols.size() + (long long)vals.size());
   plan->view.vals16 = vals16.empty() ? nullptr : (const _Float16 *)(base + off_v16);
   return plan.release();
 }
@@ -366,14 +367,14 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
 // the LDS of the cross-wave reduction within 64 KiB.
 int auto_waves(const sc_plan *p, int N) {
   if (p->npanels == 0) return 1;
-  const sc::Geometry g1 = sc::geometry(p->km, N, 1, p->K, p->view.max_pslots, p->view.max_pvals);
+  const sc::Geometry g1 = sc::geometry(p->km, N, 1, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes);
   const int S = 64 / g1.L;
   const double avg = (double)p->nslots / p->npanels;
   const double segs = (double)p->nsegs / p->npanels;
   int w_occ = (int)std::max<int64_t>(1, 4096 / std::max(1, p->npanels));
   int w_work = (int)std::max(1.0, std::max(avg / (2.0 * S), segs / 2.0));
   int w = std::min(std::min(w_occ, w_work), 16);
-  while (w > 1 && sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals).lds > 65536) --w;
+  while (w > 1 && sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes).lds > 65536) --w;
   return std::max(w, 1);
 }
 
@@ -416,7 +417,7 @@ int launch(const sc_plan *p, const sc_gen_record *rec, sc_gen_launch_fn fn, cons
       (N % 2 == 0 && ((uintptr_t)B % 8 || (uintptr_t)C % 8)) || (uintptr_t)B % 4 || (uintptr_t)C % 4)
     throw sc::Error{SC_ERR_ARG, "B and C must be aligned to their vector width (16 B when N % 4 == 0)"};
   int w = waves ? waves : (rec->waves ? rec->waves : auto_waves(p, N));
-  if (sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals).lds > 65536)
+  if (sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes).lds > 65536)
     throw sc::Error{SC_ERR_ARG, "too many waves per panel for this N"};
   sc::DevView view = p->view;
   const sc::TileGeometry tg = sc::tile_geometry(view, N);
@@ -483,7 +484,7 @@ int sc_plan_describe(const sc_plan *p, int32_t N, char *buf, size_t buflen) {
           (p->view.tnkb > 1 ? " +splitk_reduce" : "");
     } else {
       const int w = auto_waves(p, N);
-      const sc::Geometry g = sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals);
+      const sc::Geometry g = sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes);
       if (!g.wide && sc::gather_lds(N, w, p->km, p->view.max_pslots, p->view.max_pvals)) {
         d = "gather_kernel km=" + std::to_string(p->km) + " V=" + std::to_string(N) + " waves=" +
             std::to_string(w) + " grid=" + std::to_string(p->npanels);
