@@ -116,7 +116,7 @@ void sc_cfmtx_free(sc_cfmtx *cf);
 
 /* Plan flags */
 #define SC_PLAN_DROP_PADDING 1 /* omit the zero-valued padding slots on the device */
-#define SC_PLAN_TILED 2        /* also build the split-K LDS-tiled copy (opt-in)    */
+#define SC_PLAN_TILED 2        /* also build the split-K LDS-staged copy (opt-in)   */
 #define SC_PLAN_CHUNKED 4      /* build the K-block-major copy of the chunk kernel
                                   (B column chunks resident in LDS, N % 32 == 0)   */
 #define SC_PLAN_F16_VALUES 8   /* also keep a binary16 copy of the values (sc_spmm_f16) */

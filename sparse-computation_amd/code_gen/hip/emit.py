@@ -149,34 +149,69 @@ def tile_name(bits: str) -> str:
     return f"tile_{bits}"
 
 
-def emit_tile_body(km: int, bits: str, pid: int, unroll_slots: int = 8) -> str:
-    """Tiled-path body: wave-wide slots of one K block, B rows read from the
-    LDS tile.  Sub-segments are short (a segment split over K blocks), so every
-    step is a full batch of `unroll_slots`: slots past the end re-read the
-    last slot's column and contribute a zero value."""
+def _tile_step(rows, pop, slots, indent, fmas=None):
+    """Straight-line code for `slots` consecutive slots of a tile sub-segment
+    starting at slot j, values at vp.  The batch's values are read from LDS
+    once, one per lane, and each is moved to a scalar register with readlane
+    (a wave-wide broadcast read per value would cost the LDS as much as a B
+    row); the columns are read wave-wide, then the B rows, then the FMAs."""
+    out = []
+    if fmas is None:
+        nv = slots * pop
+        out.append(f"{indent}const float vl = sc::batch_values(vp, {nv});")
+        for q in range(slots):
+            for k in range(pop):
+                out.append(f"{indent}const float v{q}_{k} = sc::lane_value(vl, {q * pop + k});")
+    for q in range(slots):
+        out.append(f"{indent}const int c{q} = a.cols[j + {q}];")
+    for q in range(slots):
+        out.append(f"{indent}float b{q}[V];")
+        out.append(f"{indent}sc::load_tile<V>(b{q}, a, c{q});")
+    if fmas is None:
+        for q in range(slots):
+            for k, r in enumerate(rows):
+                out.append(f"{indent}sc::fma_row<V>(acc[{r}], v{q}_{k}, b{q});")
+    else:
+        for q in range(slots):
+            out += fmas(q, indent)
+    return out
+
+
+def _tile_loop(pop, unroll_slots, step):
+    """Full batches of `unroll_slots` slots, then the remainder in
+    power-of-two batches (4, 2, 1 for 8): no loads or FMAs past the end."""
+    U = unroll_slots
+    out = ["  int j = a.lo;",
+           "  auto vp = a.vals + a.vb;",
+           f"  for (; j + {U} <= a.hi; j += {U}, vp += {U * pop}) {{"]
+    out += step(U, "    ")
+    out.append("  }")
+    t = U // 2
+    while t >= 1:
+        out.append(f"  if (j + {t} <= a.hi) {{")
+        out += step(t, "    ")
+        out.append(f"    j += {t};")
+        out.append(f"    vp += {t * pop};")
+        out.append("  }")
+        t //= 2
+    return out
+
+
+def emit_tile_body(km: int, bits: str, pid: int, unroll_slots: int = 0) -> str:
+    """Tiled-path body: wave-wide slots of one K tile, B rows read from the
+    LDS tile, full batches of `unroll_slots` slots and a power-of-two tail.
+    By default 8 slots per batch for up to two rows, 4 above: a batch's
+    values live in scalar registers (pop per slot)."""
     rows = _rows(bits)
     pop = len(rows)
-    U = unroll_slots
+    if unroll_slots <= 0:
+        unroll_slots = 4
     out = [f"// pattern id {pid}: bits {bits} -> panel rows {', '.join(map(str, rows))} "
-           f"(pop {pop}); B rows from the LDS tile, {U} per step",
+           f"(pop {pop}); B rows from the LDS tile, {unroll_slots} per step",
            "template <int V>",
            f"__device__ __forceinline__ void {tile_name(bits)}(float (&acc)[{km}][V], "
-           "const sc::TileArgs &a) {",
-           f"  for (int j = a.lo; j < a.hi; j += {U}) {{",
-           "    const int last = a.hi - 1 - j;  // last valid offset in this batch",
-           f"    const float *vp = a.vals + a.vb + (j - a.sb) * {pop};"]
-    for q in range(U):
-        out.append(f"    const int c{q} = a.cols[j + min({q}, last)];")
-    for q in range(U):
-        out.append(f"    float b{q}[V];")
-        out.append(f"    sc::load_tile<V>(b{q}, a, c{q});")
-    for q in range(U):
-        for k in range(pop):
-            out.append(f"    const float v{q}_{k} = {q} <= last ? vp[{q * pop + k}] : 0.0f;")
-    for q in range(U):
-        for k, r in enumerate(rows):
-            out.append(f"    sc::fma_row<V>(acc[{r}], v{q}_{k}, b{q});")
-    out.append("  }")
+           "const sc::TileArgs &a) {"]
+    out += _tile_loop(pop, unroll_slots, lambda n, ind: _tile_step(rows, pop, n, ind))
     out.append("}")
     return "\n".join(out)
 
@@ -244,22 +279,37 @@ def emit_pop_bodies(km: int, pop: int, kn: int, unroll: int, unroll_slots: int =
         out.append("  }")
         t //= 2
     out.append("}")
-    # LDS tile (predicated batches)
+    # LDS tile
     out.append("template <int V, class A>")
     out.append(f"__device__ __forceinline__ void pop{pop}_tile{head} {{")
     out += _mask_rows(km, "  ")
-    out.append(f"  for (int j = a.lo; j < a.hi; j += {unroll_slots}) {{")
-    out.append("    const int last = a.hi - 1 - j;")
-    out.append(f"    const float *vp = a.vals + a.vb + (j - a.sb) * {pop};")
-    for q in range(unroll_slots):
-        out.append(f"    float b{q}[V];")
-        out.append(f"    sc::load_tile<V>(b{q}, a, a.cols[j + min({q}, last)]);")
-    for q in range(unroll_slots):
-        out += _generic_fmas(km, pop, q, "    ",
-                             lambda q_, r: f"({q_} <= last ? vp[{q_ * pop} + k{r}] : 0.0f)")
-    out.append("  }")
+    out += _tile_loop(pop, unroll_slots, lambda n, ind: _tile_step(
+        None, pop, n, ind, fmas=lambda q, i2: _generic_fmas(km, pop, q, i2, lambda q_, r: f"vp[{q_ * pop} + k{r}]")))
     out.append("}")
     return "\n".join(out)
+
+
+def _emit_tile_chain(usable, call):
+    """run_tile: the sub-segments of one (K tile, panel) record, in descending
+    row-mask order (the plan sorts them so), each run by its pattern's body.
+    The patterns are visited in that fixed order by a chain of uniform
+    branches, not a multiway switch, so the accumulators stay in place."""
+    out = ["  template <int KM, int V>",
+           "  __device__ __forceinline__ static void run_tile(const sc::lds_int4 *segs, int d, int d1,",
+           "                                                 float (&acc)[KM][V], sc::TileArgs &a) {",
+           "    sc::vec4i sd = {0, 0, 0, 0};",
+           "    if (d < d1) sd = sc::uniform4(segs[d]);"]
+    for bits, pid in sorted(usable, key=lambda bp: -_mask(bp[0])):
+        out += [f"    if (sd.x == {_mask(bits)}) {{  // id {pid}",
+                "      a.lo = sd.y;",
+                "      a.hi = sd.y + sd.z;",
+                "      a.vb = sd.w;",
+                f"      {call(bits)}",
+                "      sd.x = 0;",
+                "      if (++d < d1) sd = sc::uniform4(segs[d]);",
+                "    }"]
+    out.append("  }")
+    return out
 
 
 def sanitize(name: str) -> str:
@@ -312,8 +362,9 @@ def emit_unit(name: str, km: int, patterns, kn: int = 1, waves: int = 0, variant
             out.append(emit_pop_bodies(km, p, kn, unroll))
             out.append("")
         out.append("struct dispatch {")
-        for kind, args in (("run_tile", "sc::TileArgs"), ("run_wide", "sc::WideArgs"), ("run", None)):
-            body = {"run_tile": "tile", "run_wide": "wide", "run": "narrow"}[kind]
+        out += _emit_tile_chain(usable, lambda bits: f"pop{bits.count('1')}_tile<V>(acc, a, {_mask(bits)}u);")
+        for kind, args in (("run_wide", "sc::WideArgs"), ("run", None)):
+            body = {"run_wide": "wide", "run": "narrow"}[kind]
             if args:
                 out.append("  template <int KM, int V>")
                 out.append(f"  __device__ __forceinline__ static void {kind}(int mask, float (&acc)[KM][V], "
@@ -343,15 +394,7 @@ def emit_unit(name: str, km: int, patterns, kn: int = 1, waves: int = 0, variant
         out.append(emit_tile_body(km, bits, pid))
         out.append("")
     out.append("struct dispatch {")
-    out.append("  template <int KM, int V>")
-    out.append("  __device__ __forceinline__ static void run_tile(int mask, float (&acc)[KM][V], "
-               "const sc::TileArgs &a) {")
-    out.append("    switch (mask) {")
-    for bits, pid in usable:
-        out.append(f"      case {_mask(bits)}: {tile_name(bits)}<V>(acc, a); break;  // id {pid}")
-    out.append("      default: break;")
-    out.append("    }")
-    out.append("  }")
+    out += _emit_tile_chain(usable, lambda bits: f"{tile_name(bits)}<V>(acc, a);")
     out.append("  template <int KM, int V>")
     out.append("  __device__ __forceinline__ static void run_wide(int mask, float (&acc)[KM][V], "
                "const sc::WideArgs &a) {")

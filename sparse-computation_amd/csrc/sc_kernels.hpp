@@ -47,15 +47,18 @@ struct DevView {
   int npanels;
   int max_pslots;         // most slots in one panel
   int max_pvals;          // most values in one panel
-  // K-block-major copy of the stream for the tiled kernel (null if the plan
-  // has too little B reuse for it): for K block kb and panel p the
+  // K-block copy of the stream for the tiled and chunk kernels (null if the
+  // plan was not created for them): for K block kb and panel p the
   // sub-segments (the part of each segment whose columns fall in the block)
-  // are tseg[kp_seg[kb*(npanels+1)+p] .. kp_seg[kb*(npanels+1)+p+1]), their
-  // slots and values contiguous in tcols / tvals.
+  // are tseg[kp_seg[r] .. kp_seg[r+1]), their slots and values contiguous in
+  // tcols / tvals.  Record r of (kb, p) is kb*(npanels+1)+p for the chunk
+  // kernel (kblock_kind 2) and (rb*tnkb+kb)*tppb + p - rb*tppb, rb = p/tppb,
+  // for the tiled kernel (kblock_kind 1: row-block-major, so one unit's
+  // stream is contiguous; one sentinel record at the end).
   const int4 *tseg;       // {rowmask, slot_begin, nslots, val_begin} in tcols/tvals
-  const int *kp_seg;      // [nkb * (npanels + 1)]
-  const int *kp_slot;     // [nkb * (npanels + 1)] first tcols slot of (kb, panel)
-  const int *kp_val;      // [nkb * (npanels + 1)] first tvals value of (kb, panel)
+  const int *kp_seg;      // first sub-segment of each record (+ end)
+  const int *kp_slot;     // first tcols slot of each record (+ end)
+  const int *kp_val;      // first tvals value of each record (+ end)
   const int *tcols;
   const float *tvals;
   int tkb;                // B rows per K block
@@ -65,9 +68,14 @@ struct DevView {
   int tstage_cols;        // most slots of one (row block, K block) unit
   int tstage_vals;        // most values of one unit
   int tstage_segs;        // most sub-segments of one unit
+  int tchunk_dw;          // tiled kernel: most dwords of one (row block, K tile) chunk
+  const int *timg;        // tiled kernel: chunk images, row-block-major (LDS layout)
+  const int *toff;        // tiled kernel: first dword of chunk rb * tnkb + kb (+ end)
   long long nslots;       // slots of the whole plan
   float *work;            // split-K partial sums (plan workspace), or null
   long long work_floats;  // its size in floats
+  unsigned *tcount;       // split-K arrival counters (zero between launches), or null
+  long long tcount_n;     // their number
   int kblock_kind;        // what the K-block-major copy was built for: 0 none,
                           // 1 the split-K tiled kernel, 2 the chunk kernel
   const _Float16 *vals16; // binary16 copy of vals (SC_PLAN_F16_VALUES), or null
@@ -761,6 +769,9 @@ struct WideArgs {
 
 // Buffer descriptor word 3 for gfx9-family untyped loads (32-bit data format).
 constexpr int kBufferWord3 = 0x00020000;
+// Cache-policy operand of the buffer-load builtins: SC1 (system coherence
+// bit of gfx940-family loads and stores).
+constexpr int kCachePolicySc1 = 16;
 
 // B-row load of the wide path: the row offset col * N * 4 (< 2^32, checked at
 // launch) goes into the scalar soffset of a buffer load and the lane's column
@@ -894,38 +905,92 @@ __global__ void __launch_bounds__(1024)
 }
 
 // ---------------------------------------------------------------------------
-// Tiled path (N a multiple of 64, enough reuse): split-K with B in LDS.
-// A workgroup of W waves owns (row block of ppb panels, K block of KB B rows,
-// N chunk of 64V columns).  It stages B[k0:k0+KB, n0:n0+64V] in LDS once,
-// and the unit's slots (contiguous in the plan's K-block-major copy of the
-// stream) next to it; each wave then runs its panels' sub-segments with B
-// rows read from LDS.  Every staged B row is reused by all panels of the
-// block that touch it instead of being gathered from L2 once per slot.  With
-// more than one K block the units write partial sums to the plan's
-// workspace, summed in a fixed order by splitk_reduce (deterministic).
+// Tiled path (N a multiple of 64): split-K with double-buffered LDS stages.
+// The plan's row-block-major copy of the stream lists, for every row block of
+// kTilePanels panels and K tile of kTileRows B rows, one record per panel:
+// the part of each of the panel's pattern segments whose columns fall in the
+// tile (its sub-segments, in descending row-mask order), with tile-relative
+// columns.  The records of one (row block, tile) form a contiguous chunk.
+//
+// A workgroup of kTilePanels waves owns one unit = (row block, range of `tpu`
+// K tiles, N chunk of 64V columns); wave w owns panel rb * kTilePanels + w.
+// Each stage holds one tile's B rows and the row block's chunk for that tile
+// (header, descriptors, columns, values).  While the waves run tile t from
+// one stage, every thread already holds its share of tile t+1 in registers
+// and writes it into the other stage afterwards: one barrier per tile, and
+// the whole dependent chain of a sub-segment (descriptor, then columns and
+// values, then B rows) runs at LDS latency.  Every staged B row serves all
+// panels of the row block, where the panel kernels gather it from L2 once
+// per slot.
+//
+// With more than one K range per row block, each unit writes its partial
+// sums to the plan workspace and bumps the row block's counter; the unit that
+// arrives last adds the partials in K-range order (the result does not depend
+// on which unit is last), writes C and resets the counter for the next
+// launch.  Launches that share a plan must therefore be stream-ordered.
 // ---------------------------------------------------------------------------
+// LDS pointers of the tiled path (clang vector types: HIP's float2/float4
+// classes cannot be assigned in address space 3)
+typedef float vec2f __attribute__((ext_vector_type(2)));
+typedef float vec4f __attribute__((ext_vector_type(4)));
+typedef int vec4i __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) float lds_float;
+typedef __attribute__((address_space(3))) int lds_int;
+typedef __attribute__((address_space(3))) vec2f lds_float2;
+typedef __attribute__((address_space(3))) vec4f lds_float4;
+typedef __attribute__((address_space(3))) vec4i lds_int4;
+
+constexpr int kTileRows = 64;     // B rows per LDS tile
+constexpr int kTilePanels = 16;   // panels per row block = waves per workgroup
+// chunk header in LDS (dwords): record starts [0..kTilePanels], then the
+// offsets of the columns and of the values; descriptors start at the header's
+// end (16-byte aligned)
+constexpr int kTileChunkHeader = 20;
+constexpr int kTileHdrCols = kTilePanels + 1;
+constexpr int kTileHdrVals = kTilePanels + 2;
+constexpr int kTileMaxPerUnit = 63;  // K tiles of one unit, at most
+constexpr size_t kTileTableBytes = 3 * (kTileMaxPerUnit + 1) * sizeof(int);  // chunk table of a unit
+
+// Values read from LDS at a wave-uniform address are the same in every lane,
+// but the compiler cannot prove it: readfirstlane makes them scalar, so the
+// control flow on them stays scalar branches.
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ vec4i uniform4(vec4i x) {
+  return vec4i{uniform(x.x), uniform(x.y), uniform(x.z), uniform(x.w)};
+}
+
+// The first n (<= 64) values at vp, value i in lane i (lanes >= n read
+// value 0 and are never used).
+__device__ __forceinline__ float batch_values(const lds_float *vp, int n) {
+  const int l = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  return vp[l < n ? l : 0];
+}
+// Value i of a batch as a scalar.
+__device__ __forceinline__ float lane_value(float vl, int i) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, vl), i));
+}
+
 struct TileArgs {
-  const int *cols;     // slot columns, indexed with tcols positions
-  const float *vals;   // values, indexed with tvals positions
-  const char *lds;     // B tile, 64 * V floats per row
-  int k0;              // first B row of the tile
-  unsigned lane_off;   // lane * V * 4 bytes
-  int lo, hi;          // slot range of the sub-segment
-  int sb, vb;          // its first slot / first value
+  const lds_int *cols;    // tile-relative B row of each slot of the chunk
+  const lds_float *vals;  // values of the chunk, pop per slot
+  const lds_float *tile;  // this lane's first column in the B tile
+  int lo, hi;             // slot range [lo, hi) of the sub-segment (chunk-relative)
+  int vb;                 // its first value (chunk-relative)
 };
 
+// B row `row` of the tile: one LDS read of V floats per lane; the address is
+// one vector shift-add of the slot's row.
 template <int V>
-__device__ __forceinline__ void load_tile(float (&b)[V], const TileArgs &a, int col) {
-  constexpr unsigned row_bytes = 64u * V * 4u;
-  const float *p = reinterpret_cast<const float *>(a.lds + ((unsigned)(col - a.k0) * row_bytes + a.lane_off));
+__device__ __forceinline__ void load_tile(float (&b)[V], const TileArgs &a, int row) {
+  const lds_float *p = a.tile + (unsigned)row * (64u * V);
   if constexpr (V == 4) {
-    const float4 t = *reinterpret_cast<const float4 *>(p);
+    const vec4f t = *reinterpret_cast<const lds_float4 *>(p);
     b[0] = t.x;
     b[1] = t.y;
     b[2] = t.z;
     b[3] = t.w;
   } else if constexpr (V == 2) {
-    const float2 t = *reinterpret_cast<const float2 *>(p);
+    const vec2f t = *reinterpret_cast<const lds_float2 *>(p);
     b[0] = t.x;
     b[1] = t.y;
   } else {
@@ -933,157 +998,210 @@ __device__ __forceinline__ void load_tile(float (&b)[V], const TileArgs &a, int 
   }
 }
 
-// One workgroup per (row block, K block, N chunk).  LDS: the B tile
-// (KB x 64V floats) followed, with STAGE_A, by the unit's slot columns and
-// values (one contiguous range of the K-block-major stream).
-template <int KM, int V, bool STAGE_A, class D>
-__global__ void __launch_bounds__(1024)
-    tiled_kernel(const int4 *__restrict__ tseg, const int *__restrict__ kp_seg,
-                 const int *__restrict__ kp_slot, const int *__restrict__ kp_val,
-                 const int *__restrict__ tcols, const float *__restrict__ tvals,
+// Two workgroups per CU when both fit the LDS (V <= 2): registers are capped
+// for 8 waves per SIMD.
+template <int KM, int V, class D>
+__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(V <= 2 ? 8 : 4)))
+    tiled_kernel(const int *__restrict__ timg, const int *__restrict__ toff,
                  const float *__restrict__ B, float *__restrict__ C, float *__restrict__ work,
-                 int M, int K, int N, int npanels, int ppb, int KB, int stage_cols, int stage_vals,
-                 int accumulate, int direct) {
-  extern __shared__ float4 tile4[];
-  constexpr int NC = 64 * V;
-  const int rb = blockIdx.x;
-  const int kb = blockIdx.y;
-  const int n0 = blockIdx.z * NC;
-  const int k0 = kb * KB;
-  const int k1 = min(K, k0 + KB);
-  const int pf = rb * ppb;
-  const int pl = min(npanels, pf + ppb);
-  const int kbase = kb * (npanels + 1);
-  const int s0 = kp_slot[kbase + pf];
-  const int s1 = kp_slot[kbase + pl];
-  const int q0 = kp_val[kbase + pf];
-  const int q1 = kp_val[kbase + pl];
-  constexpr int q4 = NC / 4;
-  const int nq = (k1 - k0) * q4;
-  for (int base = threadIdx.x; base < nq; base += blockDim.x * 8) {
-    float4 r8[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int idx = min(base + u * (int)blockDim.x, nq - 1);  // nq >= 1: K block non-empty
-      const int r = idx / q4;
-      const int c = idx - r * q4;
-      r8[u] = *reinterpret_cast<const float4 *>(B + (size_t)(k0 + r) * N + n0 + c * 4);
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (base + u * blockDim.x < nq) tile4[base + u * blockDim.x] = r8[u];
-  }
-  const int *cs = tcols;
-  const float *vs = tvals;
-  const int4 *ds = tseg;
-  if constexpr (STAGE_A) {
-    // after the B tile as allocated: sub-segment descriptors, columns, values
-    const int d0u = kp_seg[kbase + pf];
-    const int d1u = kp_seg[kbase + pl];
-    int4 *ld = reinterpret_cast<int4 *>(tile4 + min(KB, K) * q4);
-    stage_copy<4>(ld, tseg + d0u, d1u - d0u);
-    int *lc = reinterpret_cast<int *>(ld + (d1u - d0u));
-    float *lv = reinterpret_cast<float *>(lc + stage_cols);
-    stage_copy<4>(lc, tcols + s0, s1 - s0);
-    stage_copy<8>(lv, tvals + q0, q1 - q0);
-    cs = lc - s0;
-    vs = lv - q0;
-    ds = ld - d0u;
-    (void)stage_vals;
-  }
-  __syncthreads();
-  const int W = blockDim.x >> 6;
+                 unsigned *__restrict__ counters, int M, int K, int N, int npanels, int ntiles,
+                 int nks, int tpu, int chunk_dw, int accumulate) {
+  extern __shared__ float4 smem4[];
+  constexpr int NC = 64 * V;                // columns of the N chunk
+  constexpr int Q4 = NC / 4;                // float4 per B-tile row
+  constexpr int TQ = kTileRows * Q4;        // float4 of one B tile
+  constexpr int NT = 64 * kTilePanels;      // threads per workgroup
+  constexpr int SPT = TQ / NT;              // B float4 staged per thread (= V)
+  static_assert(SPT * NT == TQ, "tile must split evenly over the workgroup");
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
+  const int ks = blockIdx.x % nks;
+  const int rb = blockIdx.x / nks;
+  const int n0 = blockIdx.y * NC;
+  const int panel = rb * kTilePanels + w;
+  const bool has_panel = panel < npanels;
+  const int t0 = ks * tpu;
+  const int t1 = min(ntiles, t0 + tpu);
+  const int stage_q = TQ + chunk_dw / 4;    // float4 per stage (chunk_dw % 4 == 0)
+  lds_float4 *lds4 = (lds_float4 *)smem4;
+  const vec4i *img4 = reinterpret_cast<const vec4i *>(timg);
+  // chunk table of the unit in LDS (after the two stages): first float4 of
+  // every tile's chunk and of the end
+  lds_int *table = (lds_int *)(lds4 + 2 * stage_q);
+
+  // what one thread stages: V float4 of B and one float4 of the chunk; plain
+  // copies, so the loads stay in flight while the current tile runs
+  vec4f preb[SPT];
+  vec4i prea;
+  int na = 0;  // float4 of the chunk being fetched
+  auto fetch = [&](int t) {
+#pragma unroll
+    for (int s = 0; s < SPT; ++s) {
+      const int idx = (int)threadIdx.x + s * NT;
+      const int r = idx / Q4;
+      const int c = idx - r * Q4;
+      const int row = t * kTileRows + r;
+      if (row < K) preb[s] = *reinterpret_cast<const vec4f *>(B + (size_t)row * N + n0 + c * 4);
+    }
+    const int a0 = uniform(table[t - t0]);
+    na = uniform(table[t - t0 + 1]) - a0;
+    if ((int)threadIdx.x < na) prea = img4[a0 + threadIdx.x];
+  };
+  auto put = [&](int stage, int t) {
+    lds_float4 *st = lds4 + stage * stage_q;
+#pragma unroll
+    for (int s = 0; s < SPT; ++s) {
+      const int idx = (int)threadIdx.x + s * NT;
+      if (t * kTileRows + idx / Q4 < K) st[idx] = preb[s];
+    }
+    if ((int)threadIdx.x < na) ((lds_int4 *)(st + TQ))[threadIdx.x] = prea;
+  };
+
+  float acc[KM][V];
+#pragma unroll
+  for (int r = 0; r < KM; ++r)
+#pragma unroll
+    for (int e = 0; e < V; ++e) acc[r][e] = 0.f;
+
+  const int u0 = rb * ntiles + t0;
+  if ((int)threadIdx.x <= t1 - t0) table[threadIdx.x] = toff[u0 + threadIdx.x] / 4;
+  // Pull the unit's chunks (contiguous, row-block-major) towards this XCD's
+  // L2 with one load per 64-byte line, so the stage copies of the later
+  // tiles do not each wait on HBM.
+  unsigned sink = 0;
+  {
+    const int a0 = toff[u0], a1 = toff[u0 + (t1 - t0)];
+    for (int i = a0 + (int)threadIdx.x * 16; i < a1; i += NT * 16) sink += (unsigned)timg[i];
+  }
+  __syncthreads();
+  if (t0 < t1) {
+    fetch(t0);
+    put(0, t0);
+  }
+  __syncthreads();
   TileArgs args;
-  args.cols = cs;
-  args.vals = vs;
-  args.lds = reinterpret_cast<const char *>(tile4);
-  args.k0 = k0;
-  args.lane_off = (unsigned)(lane * V * sizeof(float));
-  for (int panel = pf + w; panel < pl; panel += W) {
-    float acc[KM][V];
+  for (int t = t0; t < t1; ++t) {
+    const int stage = (t - t0) & 1;
+    const bool more = t + 1 < t1;
+    if (more) fetch(t + 1);
+    if (has_panel) {
+      const lds_float4 *st = lds4 + stage * stage_q;
+      const lds_int *a = (const lds_int *)(st + TQ);
+      args.tile = (const lds_float *)st + lane * V;
+      args.cols = a + uniform(a[kTileHdrCols]);
+      args.vals = (const lds_float *)(a + uniform(a[kTileHdrVals]));
+      D::template run_tile<KM, V>((const lds_int4 *)(a + kTileChunkHeader), uniform(a[w]), uniform(a[w + 1]),
+                                  acc, args);
+    }
+    if (more) put(stage ^ 1, t + 1);
+    __syncthreads();
+  }
+  asm volatile("" ::"v"(sink));  // keeps the prefetch loads (long complete by now)
+
+  const int row0 = panel * KM;
+  const int c0 = n0 + lane * V;
+  if (nks == 1) {
+    if (has_panel) {
+#pragma unroll
+      for (int r = 0; r < KM; ++r)
+        if (row0 + r < M) store_c<V>(C + (size_t)(row0 + r) * N + c0, acc[r], accumulate);
+    }
+    return;
+  }
+  // Partial sums go out as agent-scope atomic stores and come back as
+  // agent-scope atomic loads: both bypass the per-XCD L2 copies, so the hand
+  // over needs no L2 write-back or invalidate (which a release / acquire
+  // fence would issue, for the whole cache), only completed stores before
+  // the counter is bumped.
+  if (has_panel) {
 #pragma unroll
     for (int r = 0; r < KM; ++r)
+      if (row0 + r < M) {
+        float *dst = work + ((size_t)ks * M + row0 + r) * N + c0;
 #pragma unroll
-      for (int e = 0; e < V; ++e) acc[r][e] = 0.f;
-    const int d0 = kp_seg[kbase + panel];
-    const int d1 = kp_seg[kbase + panel + 1];
-    for (int d = d0; d < d1; ++d) {
-      const int4 sd = ds[d];
-      args.lo = sd.y;
-      args.hi = sd.y + sd.z;
-      args.sb = sd.y;
-      args.vb = sd.w;
-      D::template run_tile<KM, V>(sd.x, acc, args);
-    }
-    const int row0 = panel * KM;
-#pragma unroll
-    for (int r = 0; r < KM; ++r) {
-      if (row0 + r >= M) break;
-      if (direct)
-        store_c<V>(C + (size_t)(row0 + r) * N + n0 + lane * V, acc[r], accumulate);
-      else
-        store_c<V>(work + ((size_t)kb * M + row0 + r) * N + n0 + lane * V, acc[r], 0);
-    }
+        for (int e = 0; e < V; ++e) __hip_atomic_store(dst + e, acc[r][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
   }
-}
-
-// C = sum over K blocks of the partials (fixed order), + C when accumulating.
-template <int UNUSED = 0>  // template: defined in every unit that includes this header
-__global__ void __launch_bounds__(256) splitk_reduce(const float4 *__restrict__ work,
-                                                     float4 *__restrict__ C, long long n4, int nkb,
-                                                     int accumulate) {
-  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n4;
-       i += (long long)gridDim.x * blockDim.x) {
-    float4 s = work[i];
-    for (int k = 1; k < nkb; ++k) {
-      const float4 t = work[(size_t)k * n4 + i];
-      s.x += t.x;
-      s.y += t.y;
-      s.z += t.z;
-      s.w += t.w;
-    }
-    if (accumulate) {
-      const float4 o = C[i];
-      s.x += o.x;
-      s.y += o.y;
-      s.z += o.z;
-      s.w += o.w;
-    }
-    C[i] = s;
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+  __syncthreads();
+  int *flag = (int *)smem4;  // the B buffers are free after the last barrier
+  unsigned *cnt = counters + rb * gridDim.y + blockIdx.y;
+  if (threadIdx.x == 0) {
+    const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = old == (unsigned)(nks - 1);
   }
+  __syncthreads();
+  if (!*flag) return;
+  // The row block's chunk of C = the nks partials summed in K-range order,
+  // spread over the whole workgroup with every partial load in flight.
+  const int rbase = rb * kTilePanels * KM;
+  const int rows = min(kTilePanels * KM, M - rbase);
+  const size_t kstride = (size_t)M * N * sizeof(float);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      work, (short)0, (int)0x7fffffff, kBufferWord3);
+  for (int i = threadIdx.x; i < rows * Q4; i += NT) {
+    const int r = i / Q4;
+    const int c = i - r * Q4;
+    // byte offsets: lane part in voffset, K range in soffset (the whole
+    // workspace is below 2^31 bytes, checked at launch)
+    const unsigned off = (unsigned)(((size_t)(rbase + r) * N + n0 + c * 4) * sizeof(float));
+    vec4f sum;
+#pragma unroll 8
+    for (int k = 0; k < nks; ++k) {
+      // sc1: read the partial where it was written through, not a stale
+      // copy in this XCD's L2
+      const vec4f p = __builtin_bit_cast(vec4f, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      wr, off, (unsigned)(k * kstride), kCachePolicySc1));
+      sum = k == 0 ? p : sum + p;
+    }
+    float *dst = C + (size_t)(rbase + r) * N + n0 + c * 4;
+    if (accumulate) sum += *reinterpret_cast<const vec4f *>(dst);
+    *reinterpret_cast<vec4f *>(dst) = sum;
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 constexpr size_t kLdsBytes = 160 * 1024;  // LDS per workgroup on gfx950
 
 struct TileGeometry {
   bool use = false;
-  bool stage_a = false;
   int V = 0;        // floats per lane (64 * V columns per chunk)
   int chunks = 0;   // N chunks
-  int W = 16;       // waves per workgroup
-  size_t lds = 0;
-  long long work_floats = 0;
+  int nks = 1;      // K ranges per row block (units per row block and chunk)
+  int tpu = 0;      // K tiles per unit
+  int chunk_dw = 0; // stream dwords per stage (multiple of 4)
+  size_t lds = 0;   // two stages
+  long long work_floats = 0;  // partial sums (nks > 1)
+  long long counters = 0;     // one per (row block, chunk) when nks > 1
 };
 
 inline TileGeometry tile_geometry(const DevView &v, int N) {
   TileGeometry t;
-  if (!v.tseg || v.kblock_kind != 1 || N % 64 != 0 || v.npanels <= 0) return t;
-  const int V = (N % 128 == 0) ? 2 : 1;
-  const size_t btile = (size_t)std::min(v.tkb, v.K) * 64 * V * sizeof(float);
-  if (btile > kLdsBytes) return t;
+  if (!v.timg || v.kblock_kind != 1 || v.tkb != kTileRows || v.tppb != kTilePanels || N % 64 != 0 ||
+      v.npanels <= 0 || v.tnkb <= 0 || v.tchunk_dw > 4 * 64 * kTilePanels)
+    return t;
   t.use = true;
-  t.V = V;
-  t.chunks = N / (64 * V);
-  t.W = std::min(16, std::max(1, v.tppb));
-  const size_t abytes = ((size_t)v.tstage_cols + (size_t)v.tstage_vals) * 4 + (size_t)v.tstage_segs * 16;
-  t.stage_a = btile + abytes <= kLdsBytes;
-  t.lds = btile + (t.stage_a ? abytes : 0);
-  t.work_floats = v.tnkb > 1 ? (long long)v.tnkb * v.M * N : 0;
+  t.V = (N % 256 == 0) ? 4 : (N % 128 == 0) ? 2 : 1;
+  t.chunks = N / (64 * t.V);
+  t.chunk_dw = (v.tchunk_dw + 3) / 4 * 4;
+  t.lds = 2 * ((size_t)kTileRows * 64 * t.V + t.chunk_dw) * sizeof(float) + kTileTableBytes;
+  if (t.lds > kLdsBytes) {
+    t.use = false;
+    return t;
+  }
+  // about two workgroups per CU in flight (one when the buffers take more
+  // than half the LDS), split over the K ranges of each (row block, chunk)
+  const long long target = t.lds * 2 <= kLdsBytes ? 512 : 256;
+  const long long rbc = (long long)v.tnrb * t.chunks;
+  int nks = (int)std::max<long long>(1, std::min<long long>(v.tnkb, (target + rbc / 2) / rbc));
+  nks = std::max(nks, (v.tnkb + kTileMaxPerUnit - 1) / kTileMaxPerUnit);
+  t.tpu = (v.tnkb + nks - 1) / nks;
+  t.nks = (v.tnkb + t.tpu - 1) / t.tpu;
+  t.work_floats = t.nks > 1 ? (long long)t.nks * v.M * N : 0;
+  t.counters = t.nks > 1 ? rbc : 0;
+  if (t.work_floats * (long long)sizeof(float) >= (1ll << 31)) t.use = false;  // buffer offsets
   return t;
 }
-
 // Floats per lane of the wide path for N columns, 0 if N does not fit it.
 inline int wide_v(int N, long long K = 0) {
   if ((long long)K * N * 4 >= (1LL << 32)) return 0;
@@ -1159,28 +1277,17 @@ hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int 
                          int pack, hipStream_t stream) {
   if (v.npanels <= 0 || N <= 0) return hipSuccess;
   const TileGeometry tg = tile_geometry(v, N);
-  if (tg.use && (v.tnkb == 1 || (v.work && v.work_floats >= tg.work_floats))) {
-    dim3 tgrid((unsigned)v.tnrb, (unsigned)v.tnkb, (unsigned)tg.chunks), tblock((unsigned)(64 * tg.W));
-    const int direct = v.tnkb == 1;
-#define SC_TILED(VV, SA)                                                                             \
-  hipLaunchKernelGGL((tiled_kernel<KM, VV, SA, D>), tgrid, tblock, tg.lds, stream, v.tseg, v.kp_seg, \
-                     v.kp_slot, v.kp_val, v.tcols, v.tvals, B, C, v.work, v.M, v.K, N, v.npanels,   \
-                     v.tppb, v.tkb, v.tstage_cols, v.tstage_vals, accumulate, direct)
-    if (tg.V == 2) {
-      if (tg.stage_a) SC_TILED(2, true);
-      else SC_TILED(2, false);
-    } else {
-      if (tg.stage_a) SC_TILED(1, true);
-      else SC_TILED(1, false);
-    }
+  if (tg.use && (tg.nks == 1 || (v.work && v.work_floats >= tg.work_floats && v.tcount &&
+                                 v.tcount_n >= tg.counters))) {
+    dim3 tgrid((unsigned)(v.tnrb * tg.nks), (unsigned)tg.chunks), tblock(64u * kTilePanels);
+#define SC_TILED(VV)                                                                                  \
+  hipLaunchKernelGGL((tiled_kernel<KM, VV, D>), tgrid, tblock, tg.lds, stream, v.timg, v.toff, B, C,  \
+                     v.work, v.tcount, v.M, v.K, N, v.npanels, v.tnkb, tg.nks, tg.tpu, tg.chunk_dw,   \
+                     accumulate)
+    if (tg.V == 4) SC_TILED(4);
+    else if (tg.V == 2) SC_TILED(2);
+    else SC_TILED(1);
 #undef SC_TILED
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || direct) return e;
-    const long long n4 = (long long)v.M * N / 4;
-    const int blocks = (int)std::min<long long>(4096, (n4 + 255) / 256);
-    hipLaunchKernelGGL(splitk_reduce<0>, dim3((unsigned)blocks), dim3(256), 0, stream,
-                       reinterpret_cast<const float4 *>(v.work), reinterpret_cast<float4 *>(C), n4,
-                       v.tnkb, accumulate);
     return hipGetLastError();
   }
   if (pack == 1) {

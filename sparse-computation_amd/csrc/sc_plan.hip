@@ -59,8 +59,6 @@ const GenEntry kBuiltin[] = {
 };
 #undef SC_GEN_ENTRY
 constexpr int kMaxBuiltinKm = 6;
-constexpr int kTileRows = 256;           // B rows per K block of the tiled kernel
-constexpr double kTileMinReuse = 3.0;    // slots per staged B row to build the tiled copy
 
 void hip_check(hipError_t e, const char *what) {
   if (e != hipSuccess) throw sc::Error{SC_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e)};
@@ -81,6 +79,10 @@ struct sc_plan {
   // needs more (so that call must not be inside a HIP graph capture)
   mutable float *work = nullptr;
   mutable long long work_floats = 0;
+  // arrival counters of the split-K units (zeroed when allocated; every
+  // launch leaves them at zero)
+  mutable unsigned *tcount = nullptr;
+  mutable long long tcount_n = 0;
   sc::DevView view{};
   GenEntry gen{};
 };
@@ -184,14 +186,13 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   // K-block-major copy of the stream: for K block kb and panel p, the part
   // of each of p's segments whose columns fall in the block, contiguous per
   // (kb, p) and so per (kb, group of panels).  Built for the split-K tiled
-  // kernel (SC_PLAN_TILED, 256-row blocks, only with enough B reuse; opt-in:
-  // on the 4096^2, N=128 workload it measured slower than the wide kernel)
+  // kernel (SC_PLAN_TILED: 64-row tiles, row blocks of kTilePanels panels)
   // or for the chunk kernel (SC_PLAN_CHUNKED, 512-row blocks, groups of
   // kChunkPanels panels).  Needs every segment in ascending column order,
   // which is what the format builder writes; a file that is not gets no copy.
   const bool want_tiled = (flags & SC_PLAN_TILED) != 0;
   const bool want_chunk = (flags & SC_PLAN_CHUNKED) != 0;
-  const int tkb = want_chunk ? sc::kChunkTileRows : kTileRows;
+  const int tkb = want_chunk ? sc::kChunkTileRows : sc::kTileRows;
   const int tnkb = K > 0 ? (K + tkb - 1) / tkb : 0;
   int tnrb = 0, tppb = 0;
   bool tiled = false;
@@ -204,12 +205,10 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
         break;
       }
   if (tnkb > 0 && npanels > 0 && !cols.empty() && sorted && want_tiled) {
-    tnrb = std::max(1, std::min(npanels, 512 / tnkb));
-    tppb = (npanels + tnrb - 1) / tnrb;
+    tppb = sc::kTilePanels;
     tnrb = (npanels + tppb - 1) / tppb;
-    const double staged = (double)tnrb * tnkb * std::min(tkb, K);
-    tiled = (double)cols.size() >= kTileMinReuse * staged;
-    kind = tiled ? 1 : 0;
+    tiled = true;
+    kind = 1;
   }
   if (tnkb > 0 && npanels > 0 && !cols.empty() && sorted && want_chunk) {
     tppb = std::min(npanels, sc::kChunkPanels);
@@ -221,7 +220,83 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   std::vector<int32_t> kp_seg, kp_slot, kp_val, tcols;
   std::vector<float> tvals;
   int tstage_cols = 0, tstage_vals = 0, tstage_segs = 0;
-  if (tiled) {
+  int tchunk_dw = 0;  // most dwords of one (row block, K tile) chunk (tiled kernel)
+  std::vector<int32_t> timg, toff;  // tiled kernel: chunk images and their offsets
+  if (tiled && kind == 1) {
+    // One chunk per (row block, K tile), row-block-major, each already laid
+    // out as the kernel's LDS stage holds it (a multiple of 4 dwords):
+    //   [0 .. tppb]     first descriptor of each panel's record (+ end)
+    //   [tppb + 1]      dword offset of the columns, [tppb + 2] of the values
+    //   [header ..)     descriptors {row mask, first slot, slots, first value}
+    //                   (chunk-relative), a record's in descending mask order
+    //   columns         B row of each slot relative to the tile
+    //   values          pop per slot
+    // toff[rb * tnkb + kb] is the chunk's first dword; one sentinel at the end.
+    toff.reserve((size_t)tnrb * tnkb + 1);
+    timg.reserve((size_t)tnrb * tnkb * sc::kTileChunkHeader + 2 * cols.size() + vals.size() + 4 * seg.size());
+    std::vector<int32_t> cursor(seg.size());  // next slot of every segment
+    for (size_t si = 0; si < seg.size(); ++si) cursor[si] = seg[si].y;
+    std::vector<int4> cseg;
+    std::vector<int32_t> crec, ccol, cval;
+    for (int rb = 0; rb < tnrb; ++rb)
+      for (int kb = 0; kb < tnkb; ++kb) {
+        const int64_t klim = (int64_t)(kb + 1) * tkb;
+        cseg.clear();
+        crec.clear();
+        ccol.clear();
+        cval.clear();
+        for (int32_t q = rb * tppb; q < (rb + 1) * tppb; ++q) {
+          crec.push_back((int32_t)cseg.size());
+          if (q >= npanels) continue;
+          // sub-segments of a record in descending row-mask order: the kernel
+          // visits the patterns in that fixed order
+          std::vector<int32_t> order;
+          for (int32_t si = panel_seg[(size_t)q]; si < panel_seg[(size_t)q + 1]; ++si) order.push_back(si);
+          std::stable_sort(order.begin(), order.end(),
+                           [&](int32_t x, int32_t y) { return (unsigned)seg[(size_t)x].x > (unsigned)seg[(size_t)y].x; });
+          for (int32_t si : order) {
+            const int4 sd = seg[(size_t)si];
+            const int pop = __builtin_popcount((unsigned)sd.x);
+            const int lo = cursor[(size_t)si];
+            int hi = lo;
+            while (hi < sd.y + sd.z && cols[(size_t)hi] < klim) ++hi;
+            if (hi == lo) continue;
+            cursor[(size_t)si] = hi;
+            cseg.push_back(make_int4(sd.x, (int)ccol.size(), hi - lo, (int)cval.size()));
+            for (int j = lo; j < hi; ++j) ccol.push_back(cols[(size_t)j] - kb * tkb);  // tile-relative
+            const size_t vs = (size_t)sd.w + (size_t)(lo - sd.y) * pop;
+            for (size_t v = vs; v < vs + (size_t)(hi - lo) * pop; ++v) {
+              int32_t bits;
+              std::memcpy(&bits, &vals[v], sizeof bits);
+              cval.push_back(bits);
+            }
+          }
+        }
+        crec.push_back((int32_t)cseg.size());
+        const int64_t ocol = sc::kTileChunkHeader + 4 * (int64_t)cseg.size();
+        const int64_t oval = ocol + (int64_t)ccol.size();
+        const int64_t dw = (oval + (int64_t)cval.size() + 3) / 4 * 4;
+        if ((int64_t)timg.size() + dw > INT32_MAX) throw sc::Error{SC_ERR_UNSUPPORTED, "plan larger than int32 offsets"};
+        toff.push_back((int32_t)timg.size());
+        const size_t c0 = timg.size();
+        timg.resize(c0 + (size_t)dw, 0);
+        for (size_t i = 0; i < crec.size(); ++i) timg[c0 + i] = crec[i];
+        timg[c0 + sc::kTileHdrCols] = (int32_t)ocol;
+        timg[c0 + sc::kTileHdrVals] = (int32_t)oval;
+        for (size_t i = 0; i < cseg.size(); ++i) {
+          timg[c0 + sc::kTileChunkHeader + 4 * i + 0] = cseg[i].x;
+          timg[c0 + sc::kTileChunkHeader + 4 * i + 1] = cseg[i].y;
+          timg[c0 + sc::kTileChunkHeader + 4 * i + 2] = cseg[i].z;
+          timg[c0 + sc::kTileChunkHeader + 4 * i + 3] = cseg[i].w;
+        }
+        std::copy(ccol.begin(), ccol.end(), timg.begin() + (ptrdiff_t)(c0 + ocol));
+        std::copy(cval.begin(), cval.end(), timg.begin() + (ptrdiff_t)(c0 + oval));
+        tchunk_dw = (int)std::max<int64_t>(tchunk_dw, dw);
+      }
+    toff.push_back((int32_t)timg.size());
+    for (size_t si = 0; si < seg.size(); ++si)
+      if (cursor[si] != seg[si].y + seg[si].z) throw sc::Error{SC_ERR_INTERNAL, "tiled layout lost slots"};
+  } else if (tiled) {
     kp_seg.resize((size_t)tnkb * (npanels + 1));
     kp_slot.resize(kp_seg.size());
     kp_val.resize(kp_seg.size());
@@ -303,7 +378,9 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
     vals16.resize(vals.size());
     for (size_t i = 0; i < vals.size(); ++i) vals16[i] = (_Float16)vals[i];
   }
-  size_t off_v16 = align_up<int>(off_tvals + tvals.size() * sizeof(float));
+  size_t off_timg = align_up<int>(off_tvals + tvals.size() * sizeof(float));
+  size_t off_toff = align_up<int>(off_timg + timg.size() * sizeof(int32_t));
+  size_t off_v16 = align_up<int>(off_toff + toff.size() * sizeof(int32_t));
   size_t total = align_up<int>(off_v16 + vals16.size() * sizeof(_Float16));
   hip_check(hipMalloc(&plan->dmem, total), "hipMalloc(plan)");
   std::vector<unsigned char> host(total, 0);
@@ -320,6 +397,8 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   std::memcpy(host.data() + off_cols, cols.data(), cols.size() * sizeof(int32_t));
   std::memcpy(host.data() + off_vals, vals.data(), vals.size() * sizeof(float));
   std::memcpy(host.data() + off_v16, vals16.data(), vals16.size() * sizeof(_Float16));
+  std::memcpy(host.data() + off_timg, timg.data(), timg.size() * sizeof(int32_t));
+  std::memcpy(host.data() + off_toff, toff.data(), toff.size() * sizeof(int32_t));
   hipError_t e = hipMemcpy(plan->dmem, host.data(), total, hipMemcpyHostToDevice);
   if (e != hipSuccess) {
     (void)hipFree(plan->dmem);
@@ -338,12 +417,14 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   plan->view.npanels = npanels;
   plan->view.max_pslots = max_pp;
   plan->view.max_pvals = max_pv;
-  plan->view.tseg = tiled ? (const int4 *)(base + off_tseg) : nullptr;
+  plan->view.tseg = (tiled && kind == 2) ? (const int4 *)(base + off_tseg) : nullptr;
   plan->view.kp_seg = (const int *)(base + off_kpseg);
   plan->view.kp_slot = (const int *)(base + off_kpslot);
   plan->view.kp_val = (const int *)(base + off_kpval);
   plan->view.tcols = (const int *)(base + off_tcols);
   plan->view.tvals = (const float *)(base + off_tvals);
+  plan->view.timg = timg.empty() ? nullptr : (const int *)(base + off_timg);
+  plan->view.toff = toff.empty() ? nullptr : (const int *)(base + off_toff);
   plan->view.tkb = tkb;
   plan->view.tnkb = tnkb;
   plan->view.tppb = tppb;
@@ -351,9 +432,12 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   plan->view.tstage_cols = tstage_cols;
   plan->view.tstage_vals = tstage_vals;
   plan->view.tstage_segs = tstage_segs;
+  plan->view.tchunk_dw = tchunk_dw;
   plan->view.nslots = (long long)cols.size();
   plan->view.work = nullptr;
   plan->view.work_floats = 0;
+  plan->view.tcount = nullptr;
+  plan->view.tcount_n = 0;
   plan->view.kblock_kind = kind;
   plan->view.a_bytes = 4ll * ((long long)cols.size() + (long long)vals.size());
   plan->view.vals16 = vals16.empty() ? nullptr : (const _Float16 *)(base + off_v16);
@@ -429,8 +513,19 @@ int launch(const sc_plan *p, const sc_gen_record *rec, sc_gen_launch_fn fn, cons
               "hipMalloc(split-K workspace)");
     p->work_floats = tg.work_floats;
   }
+  if (tg.use && tg.counters > p->tcount_n) {
+    if (p->tcount) (void)hipFree(p->tcount);
+    p->tcount = nullptr;
+    p->tcount_n = 0;
+    hip_check(hipMalloc((void **)&p->tcount, (size_t)tg.counters * sizeof(unsigned)),
+              "hipMalloc(split-K counters)");
+    hip_check(hipMemset(p->tcount, 0, (size_t)tg.counters * sizeof(unsigned)), "hipMemset(split-K counters)");
+    p->tcount_n = tg.counters;
+  }
   view.work = p->work;
   view.work_floats = p->work_floats;
+  view.tcount = p->tcount;
+  view.tcount_n = p->tcount_n;
   int e = fn(&view, B, C, N, (flags & SC_ACCUMULATE) ? 1 : 0, w, stream);
   hip_check((hipError_t)e, "pattern kernel launch");
   return SC_OK;
@@ -478,10 +573,10 @@ int sc_plan_describe(const sc_plan *p, int32_t N, char *buf, size_t buflen) {
           std::to_string(cg.grid) + " (" + std::to_string(cg.ngroups) + " row groups x " +
           std::to_string(cg.nchunks) + " chunks)";
     } else if (tg.use) {
-      d = "tiled_kernel km=" + std::to_string(p->km) + " V=" + std::to_string(tg.V) + " stage_a=" +
-          std::to_string(tg.stage_a ? 1 : 0) + " waves=" + std::to_string(tg.W) + " grid=" +
-          std::to_string(p->view.tnrb) + "x" + std::to_string(p->view.tnkb) + "x" + std::to_string(tg.chunks) +
-          (p->view.tnkb > 1 ? " +splitk_reduce" : "");
+      d = "tiled_kernel km=" + std::to_string(p->km) + " V=" + std::to_string(tg.V) + " waves=" +
+          std::to_string(sc::kTilePanels) + " tile_rows=" + std::to_string(sc::kTileRows) + " grid=" +
+          std::to_string(p->view.tnrb) + "x" + std::to_string(tg.nks) + "x" + std::to_string(tg.chunks) +
+          " tiles_per_unit=" + std::to_string(tg.tpu);
     } else {
       const int w = auto_waves(p, N);
       const sc::Geometry g = sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes);
@@ -553,6 +648,7 @@ void sc_plan_destroy(sc_plan *plan) {
   if (!plan) return;
   if (plan->dmem) (void)hipFree(plan->dmem);
   if (plan->work) (void)hipFree(plan->work);
+  if (plan->tcount) (void)hipFree(plan->tcount);
   delete plan;
 }
 

@@ -193,6 +193,24 @@ def test_spmm_split_k_ragged(n, flags):
     assert O.max_rel_err(Cacc - C0.astype(np.float64), c64, cab + np.abs(C0)) <= REL_TOL
 
 
+@pytest.mark.parametrize("n", [64, 128, 256])
+def test_tiled_split_k_back_to_back_inputs(n):
+    # split-K units hand partial sums to the last unit of each row block
+    # through the plan workspace; successive launches on one plan with
+    # different B (and a different N in between) must each see only their
+    # own partials, and every launch leaves the arrival counters at zero
+    A, B1 = synth_case(1500, 2300, 0.12, n, seed=0x5EED0000 + 9100 + n)
+    B2 = sc_amd.synth_dense(2300 * n, 0x5EED0000 + 9150 + n).reshape(2300, n)
+    B3 = sc_amd.synth_dense(2300 * 64, 0x5EED0000 + 9170).reshape(2300, 64)
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1), sc_amd.PLAN_TILED)
+    assert plan.describe(n).startswith("tiled_kernel")
+    for Bx in (B1, B2, B3, B1):
+        Ct = torch.full((1500, Bx.shape[1]), float("nan"), device=DEV)
+        plan.spmm(torch.from_numpy(Bx).to(DEV), Ct)
+        torch.cuda.synchronize()
+        assert oracle_check(A, Bx, Ct.cpu().numpy())[0] <= REL_TOL
+
+
 @pytest.mark.parametrize("flags", [0, sc_amd.PLAN_TILED, sc_amd.PLAN_CHUNKED])
 def test_spmm_is_deterministic(flags):
     A, B = synth_case(4096, 4096, 0.10, 128, seed=77, structured=True)
