@@ -236,6 +236,40 @@ __device__ __forceinline__ void stage_copy(T *dst, const T *__restrict__ src, in
   }
 }
 
+// Two such copies (a panel's column indices and its values) with the loads
+// of both in flight together: one memory round trip per pass instead of one
+// per array.
+template <int U1, int U2>
+__device__ __forceinline__ void stage_copy2(int *d1, const int *__restrict__ s1, int n1, float *d2,
+                                            const float *__restrict__ s2, int n2) {
+  const int step = blockDim.x;
+  for (int pass = 0;; ++pass) {
+    const int b1 = threadIdx.x + pass * step * U1;
+    const int b2 = threadIdx.x + pass * step * U2;
+    if (b1 >= n1 && b2 >= n2) break;
+    int r1[U1];
+    float r2[U2];
+    if (n1 > 0) {
+#pragma unroll
+      for (int u = 0; u < U1; ++u) r1[u] = __builtin_nontemporal_load(&s1[min(b1 + u * step, n1 - 1)]);
+    }
+    if (n2 > 0) {
+#pragma unroll
+      for (int u = 0; u < U2; ++u) r2[u] = __builtin_nontemporal_load(&s2[min(b2 + u * step, n2 - 1)]);
+    }
+#pragma unroll
+    for (int u = 0; u < U1; ++u) keep(r1[u]);
+#pragma unroll
+    for (int u = 0; u < U2; ++u) keep(r2[u]);
+#pragma unroll
+    for (int u = 0; u < U1; ++u)
+      if (b1 + u * step < n1) d1[b1 + u * step] = r1[u];
+#pragma unroll
+    for (int u = 0; u < U2; ++u)
+      if (b2 + u * step < n2) d2[b2 + u * step] = r2[u];
+  }
+}
+
 // The panel kernel (any N; lane groups of L lanes per slot, S = 64/L slots
 // in flight per wave).  D is the generated dispatcher: D::run<KM, V>(mask,
 // acc, args) runs the straight-line body of the pattern whose row mask is
@@ -275,8 +309,7 @@ __global__ void __launch_bounds__(1024)
     const int q1 = panel_val[panel + 1];
     int *lc = reinterpret_cast<int *>(red);
     float *lv = red + stage_cols;
-    stage_copy<4>(lc, cols + p0, p1 - p0);
-    stage_copy<8>(lv, vals + q0, q1 - q0);
+    stage_copy2<4, 8>(lc, cols + p0, p1 - p0, lv, vals + q0, q1 - q0);
     __syncthreads();
     cs = lc - p0;  // indexed with global slot numbers
     vs = lv - q0;
@@ -437,8 +470,7 @@ __global__ void __launch_bounds__(1024)
     const int uv0 = kp_val[base + p0], uv1 = kp_val[base + p1];
     if (kb > 0) __syncthreads();  // every wave is done with the previous block
     stage_chunk<8>(btile, reinterpret_cast<const float4 *>(B), rows, N / 4, k0, n0 / 4);
-    stage_copy<4>(lcols, tcols + us0, us1 - us0);
-    stage_copy<8>(lvals, tvals + uv0, uv1 - uv0);
+    stage_copy2<4, 8>(lcols, tcols + us0, us1 - us0, lvals, tvals + uv0, uv1 - uv0);
     __syncthreads();
     if (has_panel) {
       args.cols = lcols - us0;  // indexed with positions in tcols / tvals
@@ -619,6 +651,52 @@ __device__ __forceinline__ void gather_rows(typename VecOf<V>::T *dst, const int
   }
 }
 
+// The fp32 small-N staging in one pipeline: the panel's values and column
+// indices are loaded together, the B rows as soon as the columns arrive (the
+// values still in flight), then everything is stored to LDS.
+template <int V, int UC, int UV>
+__device__ __forceinline__ void stage_values_gather_rows(float *lv, const float *__restrict__ vals, int nv,
+                                                         typename VecOf<V>::T *gb, const int *__restrict__ cols,
+                                                         const void *__restrict__ B, int nc) {
+  using T = typename VecOf<V>::T;
+  const T *Bv = reinterpret_cast<const T *>(B);
+  const int step = blockDim.x;
+  for (int pass = 0;; ++pass) {
+    const int bc = threadIdx.x + pass * step * UC;
+    const int bv = threadIdx.x + pass * step * UV;
+    if (bc >= nc && bv >= nv) break;
+    int c[UC];
+    float v[UV];
+    T r[UC];
+    if (nc > 0) {
+#pragma unroll
+      for (int u = 0; u < UC; ++u) c[u] = __builtin_nontemporal_load(&cols[min(bc + u * step, nc - 1)]);
+    }
+    if (nv > 0) {
+#pragma unroll
+      for (int u = 0; u < UV; ++u) v[u] = __builtin_nontemporal_load(&vals[min(bv + u * step, nv - 1)]);
+    }
+    if (nc > 0) {
+#pragma unroll
+      for (int u = 0; u < UC; ++u) keep(c[u]);
+#pragma unroll
+      for (int u = 0; u < UC; ++u) r[u] = Bv[c[u]];
+#pragma unroll
+      for (int u = 0; u < UC; ++u) keep(r[u]);
+#pragma unroll
+      for (int u = 0; u < UC; ++u)
+        if (bc + u * step < nc) gb[bc + u * step] = r[u];
+    }
+    if (nv > 0) {
+#pragma unroll
+      for (int u = 0; u < UV; ++u) keep(v[u]);
+#pragma unroll
+      for (int u = 0; u < UV; ++u)
+        if (bv + u * step < nv) lv[bv + u * step] = v[u];
+    }
+  }
+}
+
 // n binary16 values (bits) -> fp32 in dst, UNR loads in flight per thread.
 template <int UNR>
 __device__ __forceinline__ void stage_half_values(float *dst, const unsigned short *__restrict__ src, int n) {
@@ -676,11 +754,13 @@ __global__ void __launch_bounds__(1024)
   const int row0 = panel * KM;
   float *lv = smem;
   float *gb = smem + stage_vals;
-  if constexpr (HALF)
+  if constexpr (HALF) {
     stage_half_values<8>(lv, reinterpret_cast<const unsigned short *>(vals) + q0, q1 - q0);
-  else
-    stage_copy<8>(lv, reinterpret_cast<const float *>(vals) + q0, q1 - q0);
-  gather_rows<V, 8, HALF>(reinterpret_cast<typename VecOf<V>::T *>(gb), cols + p0, B, p1 - p0);
+    gather_rows<V, 8, HALF>(reinterpret_cast<typename VecOf<V>::T *>(gb), cols + p0, B, p1 - p0);
+  } else {
+    stage_values_gather_rows<V, 8, 8>(lv, reinterpret_cast<const float *>(vals) + q0, q1 - q0,
+                                      reinterpret_cast<typename VecOf<V>::T *>(gb), cols + p0, B, p1 - p0);
+  }
   __syncthreads();
 
   GatherArgs args;
@@ -829,8 +909,7 @@ __global__ void __launch_bounds__(1024)
     const int q1 = panel_val[panel + 1];
     int *lc = reinterpret_cast<int *>(smem);
     float *lv = smem + stage_cols;
-    stage_copy<4>(lc, cols + p0, p1 - p0);
-    stage_copy<8>(lv, vals + q0, q1 - q0);
+    stage_copy2<4, 8>(lc, cols + p0, p1 - p0, lv, vals + q0, q1 - q0);
     __syncthreads();
     cs = lc - p0;  // indexed with global slot numbers
     vs = lv - q0;
@@ -896,8 +975,7 @@ __global__ void __launch_bounds__(1024)
         const int q1 = panel_val[panel + 1];
         int *lc = reinterpret_cast<int *>(smem);
         float *lv = smem + stage_cols;
-        stage_copy<4>(lc, cols + p0, p1 - p0);
-        stage_copy<8>(lv, vals + q0, q1 - q0);
+        stage_copy2<4, 8>(lc, cols + p0, p1 - p0, lv, vals + q0, q1 - q0);
         __syncthreads();
       }
     }
