@@ -312,6 +312,36 @@ def _emit_tile_chain(usable, call):
     return out
 
 
+def _emit_seg_chain(usable, name, targs, call):
+    """run_segs: a panel's segment descriptors (SegLanes, in
+    descending row-mask order), each clipped to the wave's slot range [a0, a1)
+    and run by its pattern's body.  The patterns are visited in that fixed
+    order by a chain of uniform branches, not a multiway switch, so the
+    accumulators stay in place; a repeated mask is run again."""
+    out = [f"  template <{targs}>",
+           f"  __device__ __forceinline__ static void {name}(const sc::SegLanes &segs, int n, int a0, int a1,",
+           "                                                 float (&acc)[KM][V], A &a) {",
+           "    int i = 0;",
+           "    sc::vec4i sd = {0, 0, 0, 0};",
+           "    if (i < n) sd = segs(i);"]
+    for bits, pid in sorted(usable, key=lambda bp: -_mask(bp[0])):
+        out += [f"    while (sd.x == {_mask(bits)}) {{  // id {pid}",
+                "      const int lo = max(sd.y, a0);",
+                "      const int hi = min(sd.y + sd.z, a1);",
+                "      if (lo < hi) {",
+                "        a.lo = lo;",
+                "        a.hi = hi;",
+                "        a.sb = sd.y;",
+                "        a.vb = sd.w;",
+                f"        {call(bits)}",
+                "      }",
+                "      sd.x = 0;",
+                "      if (++i < n) sd = segs(i);",
+                "    }"]
+    out.append("  }")
+    return out
+
+
 def sanitize(name: str) -> str:
     return re.sub(r"[^0-9A-Za-z_]", "_", name)
 
@@ -363,6 +393,8 @@ def emit_unit(name: str, km: int, patterns, kn: int = 1, waves: int = 0, variant
             out.append("")
         out.append("struct dispatch {")
         out += _emit_tile_chain(usable, lambda bits: f"pop{bits.count('1')}_tile<V>(acc, a, {_mask(bits)}u);")
+        out += _emit_seg_chain(usable, "run_segs", "int KM, int V, class A",
+                               lambda bits: f"pop{bits.count('1')}_narrow<V, A>(acc, a, {_mask(bits)}u);")
         for kind, args in (("run_wide", "sc::WideArgs"), ("run", None)):
             body = {"run_wide": "wide", "run": "narrow"}[kind]
             if args:
@@ -395,6 +427,8 @@ def emit_unit(name: str, km: int, patterns, kn: int = 1, waves: int = 0, variant
         out.append("")
     out.append("struct dispatch {")
     out += _emit_tile_chain(usable, lambda bits: f"{tile_name(bits)}<V>(acc, a);")
+    out += _emit_seg_chain(usable, "run_segs", "int KM, int V, class A",
+                           lambda bits: f"{body_name(bits)}<V, A>(acc, a);")
     out.append("  template <int KM, int V>")
     out.append("  __device__ __forceinline__ static void run_wide(int mask, float (&acc)[KM][V], "
                "const sc::WideArgs &a) {")

@@ -33,6 +33,12 @@
 
 namespace sc {
 
+// Clang vector types (HIP's float2/float4 classes cannot be assigned in
+// LDS address space 3).
+typedef float vec2f __attribute__((ext_vector_type(2)));
+typedef float vec4f __attribute__((ext_vector_type(4)));
+typedef int vec4i __attribute__((ext_vector_type(4)));
+
 // Device view of a plan: the .cfmtx flattened panel-major.
 struct DevView {
   const int4 *seg;        // per segment {rowmask, slot_begin, nslots, val_begin}
@@ -87,6 +93,32 @@ struct DevView {
 constexpr int kChunkCols = 32;
 constexpr int kChunkTileRows = 512;
 constexpr int kChunkPanels = 16;
+
+// The segment descriptors of a panel, descriptor i of a group of up to 64 in
+// lane i: one vector load per group instead of a scalar round trip per
+// segment; the generated dispatchers read each back as scalars (readlane).
+// A panel's segments are in descending row-mask order (the plan sorts them),
+// the order in which the dispatchers visit the patterns.
+struct SegLanes {
+  int x, y, z, w;
+  __device__ __forceinline__ vec4i operator()(int i) const {
+    return vec4i{__builtin_amdgcn_readlane(x, i), __builtin_amdgcn_readlane(y, i),
+                 __builtin_amdgcn_readlane(z, i), __builtin_amdgcn_readlane(w, i)};
+  }
+};
+
+__device__ __forceinline__ SegLanes load_seg_lanes(const int4 *__restrict__ seg, int s0, int n) {
+  const int l = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  SegLanes r{0, 0, 0, 0};
+  if (l < n) {
+    const int4 d = seg[s0 + l];
+    r.x = d.x;
+    r.y = d.y;
+    r.z = d.z;
+    r.w = d.w;
+  }
+  return r;
+}
 
 // Everything a pattern body needs for one (segment, wave) range.
 struct SegArgs {
@@ -330,17 +362,9 @@ __global__ void __launch_bounds__(1024)
     for (int r = 0; r < KM; ++r)
 #pragma unroll
       for (int e = 0; e < V; ++e) acc[r][e] = 0.f;
-    for (int si = sg0; si < sg1; ++si) {
-      const int4 sd = seg[si];
-      const int lo = max(sd.y, a0);
-      const int hi = min(sd.y + sd.z, a1);
-      if (lo < hi) {
-        args.lo = lo;
-        args.hi = hi;
-        args.sb = sd.y;
-        args.vb = sd.w;
-        D::template run<KM, V>(sd.x, acc, args);
-      }
+    for (int g = sg0; g < sg1; g += 64) {
+      const int n = min(64, sg1 - g);
+      D::template run_segs<KM, V>(load_seg_lanes(seg, g, n), n, a0, a1, acc, args);
     }
     reduce_slot_lanes<KM, V>(acc, L);
     if (W == 1) {
@@ -774,17 +798,9 @@ __global__ void __launch_bounds__(1024)
   for (int r = 0; r < KM; ++r)
 #pragma unroll
     for (int e = 0; e < V; ++e) acc[r][e] = 0.f;
-  for (int si = sg0; si < sg1; ++si) {
-    const int4 sd = seg[si];
-    const int lo = max(sd.y, a0);
-    const int hi = min(sd.y + sd.z, a1);
-    if (lo < hi) {
-      args.lo = lo;
-      args.hi = hi;
-      args.sb = sd.y;
-      args.vb = sd.w;
-      D::template run<KM, V>(sd.x, acc, args);
-    }
+  for (int g = sg0; g < sg1; g += 64) {
+    const int n = min(64, sg1 - g);
+    D::template run_segs<KM, V>(load_seg_lanes(seg, g, n), n, a0, a1, acc, args);
   }
   reduce_slot_lanes<KM, V>(acc, 1);
   if (W == 1) {
@@ -909,7 +925,8 @@ __global__ void __launch_bounds__(1024)
     const int q1 = panel_val[panel + 1];
     int *lc = reinterpret_cast<int *>(smem);
     float *lv = smem + stage_cols;
-    stage_copy2<4, 8>(lc, cols + p0, p1 - p0, lv, vals + q0, q1 - q0);
+    stage_copy<4>(lc, cols + p0, p1 - p0);
+    stage_copy<8>(lv, vals + q0, q1 - q0);
     __syncthreads();
     cs = lc - p0;  // indexed with global slot numbers
     vs = lv - q0;
@@ -931,6 +948,9 @@ __global__ void __launch_bounds__(1024)
     for (int r = 0; r < KM; ++r)
 #pragma unroll
       for (int e = 0; e < V; ++e) acc[r][e] = 0.f;
+    // A wave's slot range meets only a few of the panel's segments: the
+    // others are skipped on the descriptor alone (scalar loads, shared by the
+    // panel's waves through the scalar cache).
     for (int si = sg0; si < sg1; ++si) {
       const int4 sd = seg[si];
       const int lo = max(sd.y, a0);
@@ -975,7 +995,8 @@ __global__ void __launch_bounds__(1024)
         const int q1 = panel_val[panel + 1];
         int *lc = reinterpret_cast<int *>(smem);
         float *lv = smem + stage_cols;
-        stage_copy2<4, 8>(lc, cols + p0, p1 - p0, lv, vals + q0, q1 - q0);
+        stage_copy<4>(lc, cols + p0, p1 - p0);
+        stage_copy<8>(lv, vals + q0, q1 - q0);
         __syncthreads();
       }
     }
@@ -1007,11 +1028,7 @@ __global__ void __launch_bounds__(1024)
 // on which unit is last), writes C and resets the counter for the next
 // launch.  Launches that share a plan must therefore be stream-ordered.
 // ---------------------------------------------------------------------------
-// LDS pointers of the tiled path (clang vector types: HIP's float2/float4
-// classes cannot be assigned in address space 3)
-typedef float vec2f __attribute__((ext_vector_type(2)));
-typedef float vec4f __attribute__((ext_vector_type(4)));
-typedef int vec4i __attribute__((ext_vector_type(4)));
+// LDS pointers of the tiled path
 typedef __attribute__((address_space(3))) float lds_float;
 typedef __attribute__((address_space(3))) int lds_int;
 typedef __attribute__((address_space(3))) vec2f lds_float2;

@@ -142,7 +142,12 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
       throw sc::Error{SC_ERR_UNSUPPORTED, "no kernel body for pattern " + p.bits};
   }
 
-  // flatten panel-major
+  // flatten panel-major, a panel's segments in descending row-mask order: the
+  // generated dispatchers visit the patterns in that fixed order
+  std::vector<size_t> pat_order(cf.patterns.size());
+  for (size_t i = 0; i < pat_order.size(); ++i) pat_order[i] = i;
+  std::stable_sort(pat_order.begin(), pat_order.end(),
+                   [&](size_t x, size_t y) { return info[x].mask > info[y].mask; });
   std::vector<int4> seg;
   std::vector<int32_t> panel_seg((size_t)npanels + 1), panel_slot((size_t)npanels + 1);
   std::vector<int32_t> panel_val((size_t)npanels + 1);
@@ -154,7 +159,7 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
     panel_seg[(size_t)q] = (int32_t)seg.size();
     panel_slot[(size_t)q] = (int32_t)cols.size();
     panel_val[(size_t)q] = (int32_t)vals.size();
-    for (size_t i = 0; i < cf.patterns.size(); ++i) {
+    for (size_t i : pat_order) {
       const sc::Pattern &p = cf.patterns[i];
       const int pop = info[i].pop;
       int32_t a = p.rpp[(size_t)q], b = p.rpp[(size_t)q + 1];
