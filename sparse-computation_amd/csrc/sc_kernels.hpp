@@ -33,6 +33,12 @@
 
 namespace sc {
 
+// Buffer descriptor word 3 for gfx9-family untyped loads (32-bit data format).
+constexpr int kBufferWord3 = 0x00020000;
+// Cache-policy operand of the buffer-load builtins: SC1 (system coherence
+// bit of gfx940-family loads and stores).
+constexpr int kCachePolicySc1 = 16;
+
 // Clang vector types (HIP's float2/float4 classes cannot be assigned in
 // LDS address space 3).
 typedef float vec2f __attribute__((ext_vector_type(2)));
@@ -133,21 +139,51 @@ struct SegArgs {
   bool cval;                     // this lane's column group lies inside N
 };
 
+// Lanes whose column group lies past N read the last full group instead
+// (Bc clamped, always in bounds) and are never stored, so the loads need no
+// branch.
 template <int V>
 __device__ __forceinline__ void load_b(float (&b)[V], const SegArgs &a, int col) {
   const float *p = a.Bc + (size_t)col * (size_t)a.N;
   if constexpr (V == 4) {
-    float4 t = a.cval ? *reinterpret_cast<const float4 *>(p) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 t = *reinterpret_cast<const float4 *>(p);
     b[0] = t.x;
     b[1] = t.y;
     b[2] = t.z;
     b[3] = t.w;
   } else if constexpr (V == 2) {
-    float2 t = a.cval ? *reinterpret_cast<const float2 *>(p) : make_float2(0.f, 0.f);
+    const float2 t = *reinterpret_cast<const float2 *>(p);
     b[0] = t.x;
     b[1] = t.y;
   } else {
-    b[0] = a.cval ? *p : 0.f;
+    b[0] = *p;
+  }
+}
+
+// The same body arguments with B read through a buffer descriptor (B below
+// 4 GiB): the B-row address is one 32-bit multiply-add (row * N * 4 plus the
+// lane's column bytes), not 64-bit pointer arithmetic.
+struct SegArgsBuf : SegArgs {
+  __amdgpu_buffer_rsrc_t Bbuf;  // whole B
+  unsigned voff;                // this lane's (clamped) column group, bytes
+  unsigned row_bytes;           // N * 4
+};
+
+template <int V>
+__device__ __forceinline__ void load_b(float (&b)[V], const SegArgsBuf &a, int col) {
+  const unsigned off = (unsigned)col * a.row_bytes + a.voff;
+  if constexpr (V == 4) {
+    const float4 t = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(a.Bbuf, off, 0, 0));
+    b[0] = t.x;
+    b[1] = t.y;
+    b[2] = t.z;
+    b[3] = t.w;
+  } else if constexpr (V == 2) {
+    const float2 t = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(a.Bbuf, off, 0, 0));
+    b[0] = t.x;
+    b[1] = t.y;
+  } else {
+    b[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(a.Bbuf, off, 0, 0));
   }
 }
 
@@ -308,12 +344,12 @@ __device__ __forceinline__ void stage_copy2(int *d1, const int *__restrict__ s1,
 // `mask`.  blockDim.x = 64 * W.  With STAGE the panel's columns and values
 // are first copied to LDS (batched loads), and the same LDS is reused for the
 // cross-wave reduction.
-template <int KM, int V, bool STAGE, class D>
+template <int KM, int V, bool STAGE, class D, class A>
 __global__ void __launch_bounds__(1024)
     panel_kernel(const int4 *__restrict__ seg, const int *__restrict__ panel_seg,
                  const int *__restrict__ panel_slot, const int *__restrict__ panel_val,
                  const int *__restrict__ cols, const float *__restrict__ vals,
-                 const float *__restrict__ B, float *__restrict__ C, int M, int N, int L,
+                 const float *__restrict__ B, float *__restrict__ C, int M, int K, int N, int L,
                  int accumulate, int pack, int stage_cols) {
   extern __shared__ float red[];
   const int panel = blockIdx.x;
@@ -349,14 +385,21 @@ __global__ void __launch_bounds__(1024)
   if constexpr (STAGE) stage();
   for (int cbase = 0; cbase < N; cbase += LV) {
     const int c0 = cbase + g * V;
-    SegArgs args;
+    const int cl = min(c0, N - V);  // lanes past N read the last group, never stored
+    A args;
     args.cols = cs;
     args.vals = vs;
-    args.Bc = B + c0;
+    args.Bc = B + cl;
     args.N = N;
     args.s = s;
     args.S = S;
     args.cval = c0 < N;
+    if constexpr (std::is_same<A, SegArgsBuf>::value) {
+      args.Bbuf = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(B), (short)0,
+                                                    (int)((size_t)K * N * sizeof(float)), kBufferWord3);
+      args.voff = (unsigned)(cl * sizeof(float));
+      args.row_bytes = (unsigned)(N * sizeof(float));
+    }
     float acc[KM][V];
 #pragma unroll
     for (int r = 0; r < KM; ++r)
@@ -863,11 +906,6 @@ struct WideArgs {
   int sb, vb;  // first slot / first value of the segment
 };
 
-// Buffer descriptor word 3 for gfx9-family untyped loads (32-bit data format).
-constexpr int kBufferWord3 = 0x00020000;
-// Cache-policy operand of the buffer-load builtins: SC1 (system coherence
-// bit of gfx940-family loads and stores).
-constexpr int kCachePolicySc1 = 16;
 
 // B-row load of the wide path: the row offset col * N * 4 (< 2^32, checked at
 // launch) goes into the scalar soffset of a buffer load and the lane's column
@@ -1330,7 +1368,16 @@ inline Geometry geometry(int km, int N, int W, long long K = 0, int max_pslots =
   Geometry g;
   g.stage = false;
   g.stage_cols = 0;
-  const int wv = wide_v(N, K);
+  int wv = wide_v(N, K);
+  // A plan streamed from HBM (one that is staged) at N = 64 or 128: the lanes-
+  // over-slots kernel with 16-byte B loads (two or four slots per wave) beats
+  // the wide kernel's 8- or 4-byte ones.  Its B-row gathers are bound by the
+  // number of requests in flight, not by bytes: 4096^2 at 10 %, N = 128:
+  // 22.2 us against 30.9.  L2-resident plans stay wide (FFN 2048x512 at 50 %,
+  // N = 128: 11.0 us against 14.3 lanes-over-slots).
+  if ((wv == 1 || wv == 2) && max_pslots >= 0 && a_bytes >= kStageMinBytes &&
+      ((size_t)(max_pslots + 3) / 4 * 4 + (size_t)max_pvals) * 4 <= kStageLimit)
+    wv = 0;
   if (wv) {
     g.wide = true;
     g.V = wv;
@@ -1425,18 +1472,32 @@ hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int 
 #undef SC_GATHER
     return hipGetLastError();
   }
-#define SC_NARROW(VV, ST)                                                                          \
-  hipLaunchKernelGGL((panel_kernel<KM, VV, ST, D>), grid, block, g.lds, stream, v.seg, v.panel_seg,  \
-                     v.panel_slot, v.panel_val, v.cols, v.vals, B, C, v.M, N, g.L, accumulate, pack, \
+#define SC_NARROW(VV, ST, AA)                                                                          \
+  hipLaunchKernelGGL((panel_kernel<KM, VV, ST, D, AA>), grid, block, g.lds, stream, v.seg, v.panel_seg,  \
+                     v.panel_slot, v.panel_val, v.cols, v.vals, B, C, v.M, v.K, N, g.L, accumulate, pack, \
                      g.stage_cols)
-  if (g.stage) {
-    if (g.V == 4) SC_NARROW(4, true);
-    else if (g.V == 2) SC_NARROW(2, true);
-    else SC_NARROW(1, true);
+  // B below 4 GiB: byte offsets fit the buffer descriptor's 32 bits
+  const bool buf = (long long)v.K * N * (long long)sizeof(float) < (1ll << 31);
+  if (buf) {
+    if (g.stage) {
+      if (g.V == 4) SC_NARROW(4, true, SegArgsBuf);
+      else if (g.V == 2) SC_NARROW(2, true, SegArgsBuf);
+      else SC_NARROW(1, true, SegArgsBuf);
+    } else {
+      if (g.V == 4) SC_NARROW(4, false, SegArgsBuf);
+      else if (g.V == 2) SC_NARROW(2, false, SegArgsBuf);
+      else SC_NARROW(1, false, SegArgsBuf);
+    }
   } else {
-    if (g.V == 4) SC_NARROW(4, false);
-    else if (g.V == 2) SC_NARROW(2, false);
-    else SC_NARROW(1, false);
+    if (g.stage) {
+      if (g.V == 4) SC_NARROW(4, true, SegArgs);
+      else if (g.V == 2) SC_NARROW(2, true, SegArgs);
+      else SC_NARROW(1, true, SegArgs);
+    } else {
+      if (g.V == 4) SC_NARROW(4, false, SegArgs);
+      else if (g.V == 2) SC_NARROW(2, false, SegArgs);
+      else SC_NARROW(1, false, SegArgs);
+    }
   }
 #undef SC_NARROW
   return hipGetLastError();
