@@ -1362,22 +1362,27 @@ constexpr size_t kStageLimit = 64 * 1024;
 // faster unstaged (FFN 2048x512 at 50 %: 11.4 vs 12.7 us; 512^2 at 10 %,
 // N=32: 7.3 vs 7.9 us).
 constexpr long long kStageMinBytes = 8ll << 20;
+// Panels with at least this many slots on average amortize the staging copy
+// even when the plan is L2-resident (lanes-over-slots kernel).
+constexpr long long kLongPanelSlots = 1000;
 
 inline Geometry geometry(int km, int N, int W, long long K = 0, int max_pslots = -1,
-                         int max_pvals = -1, long long a_bytes = -1) {
+                         int max_pvals = -1, long long a_bytes = -1, long long avg_pslots = -1) {
   Geometry g;
   g.stage = false;
   g.stage_cols = 0;
   int wv = wide_v(N, K);
-  // A plan streamed from HBM (one that is staged) at N = 64 or 128: the lanes-
-  // over-slots kernel with 16-byte B loads (two or four slots per wave) beats
-  // the wide kernel's 8- or 4-byte ones.  Its B-row gathers are bound by the
-  // number of requests in flight, not by bytes: 4096^2 at 10 %, N = 128:
-  // 22.2 us against 30.9.  L2-resident plans stay wide (FFN 2048x512 at 50 %,
-  // N = 128: 11.0 us against 14.3 lanes-over-slots).
-  if ((wv == 1 || wv == 2) && max_pslots >= 0 && a_bytes >= kStageMinBytes &&
-      ((size_t)(max_pslots + 3) / 4 * 4 + (size_t)max_pvals) * 4 <= kStageLimit)
-    wv = 0;
+  // A plan streamed from HBM, or one with long panels, at N = 64 or 128: the
+  // staged lanes-over-slots kernel with 16-byte B loads (two or four slots per
+  // wave) beats the wide kernel's 8- or 4-byte ones.  Its B-row gathers are
+  // bound by the number of requests in flight, not by bytes: 4096^2 at 10 %,
+  // N = 128: 22.2 us against 30.9; FFN 512x2048 at 50 % (1900 slots a panel):
+  // 13.8 against 17.0.  Other L2-resident plans stay wide (FFN 2048x512 at
+  // 50 %, 480 slots a panel: 11.0 us against 14.3; 512x2048 at 90 %, 700
+  // slots a panel: 9.1 against 9.5).
+  const bool long_panels = avg_pslots >= kLongPanelSlots;
+  const bool stage_fits = max_pslots >= 0 && ((size_t)(max_pslots + 3) / 4 * 4 + (size_t)max_pvals) * 4 <= kStageLimit;
+  if ((wv == 1 || wv == 2) && stage_fits && (a_bytes >= kStageMinBytes || long_panels)) wv = 0;
   if (wv) {
     g.wide = true;
     g.V = wv;
@@ -1402,7 +1407,7 @@ inline Geometry geometry(int km, int N, int W, long long K = 0, int max_pslots =
   while (g.L < groups && g.L < 64) g.L <<= 1;
   const size_t red = W > 1 ? (size_t)W * km * g.L * g.V * sizeof(float) : 0;
   g.lds = red;
-  if (max_pslots >= 0 && (a_bytes < 0 || a_bytes >= kStageMinBytes)) {
+  if (max_pslots >= 0 && (a_bytes < 0 || a_bytes >= kStageMinBytes || long_panels)) {
     const int sc = (max_pslots + 3) / 4 * 4;
     const size_t st = ((size_t)sc + (size_t)max_pvals) * 4;
     if (st <= kStageLimit) {
@@ -1442,7 +1447,7 @@ hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int 
       return hipGetLastError();
     }
   }
-  const Geometry g = geometry(KM, N, W, v.K, v.max_pslots, v.max_pvals, v.a_bytes);
+  const Geometry g = geometry(KM, N, W, v.K, v.max_pslots, v.max_pvals, v.a_bytes, v.nslots / v.npanels);
   dim3 grid((unsigned)v.npanels), block((unsigned)(64 * W));
   if (g.wide) {
 #define SC_WIDE(VV, ST)                                                                           \

@@ -3,7 +3,7 @@
 // A plan is the .cfmtx flattened panel-major for one device:
 //   seg[]         {rowmask, slot_begin, nslots, val_begin} of every non-empty
 //                 (panel, pattern) segment, panels in order, patterns in
-//                 data-block order inside a panel;
+//                 descending row-mask order inside a panel;
 //   panel_seg[]   segment range of each panel;
 //   panel_slot[]  slot range of each panel;
 //   cols[]        int32 column (B row) of every slot;
@@ -456,7 +456,8 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
 // the LDS of the cross-wave reduction within 64 KiB.
 int auto_waves(const sc_plan *p, int N) {
   if (p->npanels == 0) return 1;
-  const sc::Geometry g1 = sc::geometry(p->km, N, 1, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes);
+  const sc::Geometry g1 = sc::geometry(p->km, N, 1, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes,
+                                   p->nslots / std::max(1, p->npanels));
   const int S = 64 / g1.L;
   const double avg = (double)p->nslots / p->npanels;
   const double segs = (double)p->nsegs / p->npanels;
@@ -467,7 +468,8 @@ int auto_waves(const sc_plan *p, int N) {
   // W * N; on 512^2 at 80 % sparsity, km 4, N = 4, 4 waves run in 6.5 us
   // against 7.2 with 7
   if ((N == 2 || N == 4) && sc::gather_lds(N, 1, p->km, p->view.max_pslots, p->view.max_pvals)) w = std::min(w, 4);
-  while (w > 1 && sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes).lds > 65536) --w;
+  while (w > 1 && sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes,
+                                   p->nslots / std::max(1, p->npanels)).lds > 65536) --w;
   return std::max(w, 1);
 }
 
@@ -510,7 +512,8 @@ int launch(const sc_plan *p, const sc_gen_record *rec, sc_gen_launch_fn fn, cons
       (N % 2 == 0 && ((uintptr_t)B % 8 || (uintptr_t)C % 8)) || (uintptr_t)B % 4 || (uintptr_t)C % 4)
     throw sc::Error{SC_ERR_ARG, "B and C must be aligned to their vector width (16 B when N % 4 == 0)"};
   int w = waves ? waves : (rec->waves ? rec->waves : auto_waves(p, N));
-  if (sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes).lds > 65536)
+  if (sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes,
+                                   p->nslots / std::max(1, p->npanels)).lds > 65536)
     throw sc::Error{SC_ERR_ARG, "too many waves per panel for this N"};
   sc::DevView view = p->view;
   const sc::TileGeometry tg = sc::tile_geometry(view, N);
@@ -588,7 +591,8 @@ int sc_plan_describe(const sc_plan *p, int32_t N, char *buf, size_t buflen) {
           " tiles_per_unit=" + std::to_string(tg.tpu);
     } else {
       const int w = auto_waves(p, N);
-      const sc::Geometry g = sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes);
+      const sc::Geometry g = sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes,
+                                   p->nslots / std::max(1, p->npanels));
       if (!g.wide && sc::gather_lds(N, w, p->km, p->view.max_pslots, p->view.max_pvals)) {
         d = "gather_kernel km=" + std::to_string(p->km) + " V=" + std::to_string(N) + " waves=" +
             std::to_string(w) + " grid=" + std::to_string(p->npanels);
