@@ -168,6 +168,29 @@ def test_plan_rejects_bad_device_buffer_shapes():
         plan.spmm(torch.zeros((63, 4), device=DEV))
 
 
+@pytest.mark.parametrize("n", [96, 128])
+def test_spmm_b_above_2_gib(n):
+    # B of more than 2 GiB (n = 128: more than 4 GiB): byte offsets no longer
+    # fit a buffer descriptor, so the lanes-over-slots kernel reads B through
+    # 64-bit pointers (and the wide kernel hands N = 128 over to it); a skinny
+    # A with a few thousand entries spread over all of K
+    K = (2 ** 31 // (4 * n) + 4099) if n == 96 else (2 ** 32 // (4 * n) + 4099)
+    A = sc_amd.Csr.synth_uniform(64, K, 3000 / (64 * K), 0.05, 0x5EED0000 + 9800 + n)
+    gen = torch.Generator(device=DEV).manual_seed(n)
+    Bt = torch.empty((K, n), dtype=torch.float32, device=DEV).uniform_(-1.0, 1.0, generator=gen)
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1))
+    assert plan.describe(n).startswith("panel_kernel")
+    C = plan.spmm(Bt)
+    torch.cuda.synchronize()
+    # the oracle on the B rows A touches only
+    ip, ix, ax = csr_f32(A)
+    used, local = np.unique(ix, return_inverse=True)
+    Bs = Bt.index_select(0, torch.from_numpy(used.astype(np.int64)).to(DEV)).cpu().numpy()
+    del Bt
+    c64, cab = O.spmm_f64(64, n, ip, local.astype(np.int32), ax, Bs)
+    assert O.max_rel_err(C.cpu().numpy(), c64, cab) <= REL_TOL
+
+
 def test_spmm_wide_unstaged_dense_panels():
     # panels of km=6 rows over 4096 dense-ish columns hold more than 64 KiB of
     # stream, so the wide kernel reads columns/values from global memory
