@@ -467,7 +467,7 @@ int auto_waves(const sc_plan *p, int N) {
   // small-N gather kernel at N = 2, 4: the cross-wave reduction grows with
   // W * N; on 512^2 at 80 % sparsity, km 4, N = 4, 4 waves run in 6.5 us
   // against 7.2 with 7
-  if ((N == 2 || N == 4) && sc::gather_lds(N, 1, p->km, p->view.max_pslots, p->view.max_pvals)) w = std::min(w, 4);
+  if ((N == 2 || N == 4) && sc::gather_lds_f32(N, 1, p->km, p->view.max_pslots, p->view.max_pvals)) w = std::min(w, 4);
   while (w > 1 && sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes,
                                    p->nslots / std::max(1, p->npanels)).lds > 65536) --w;
   return std::max(w, 1);
@@ -593,7 +593,7 @@ int sc_plan_describe(const sc_plan *p, int32_t N, char *buf, size_t buflen) {
       const int w = auto_waves(p, N);
       const sc::Geometry g = sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes,
                                    p->nslots / std::max(1, p->npanels));
-      if (!g.wide && sc::gather_lds(N, w, p->km, p->view.max_pslots, p->view.max_pvals)) {
+      if (!g.wide && sc::gather_lds_f32(N, w, p->km, p->view.max_pslots, p->view.max_pvals)) {
         d = "gather_kernel km=" + std::to_string(p->km) + " V=" + std::to_string(N) + " waves=" +
             std::to_string(w) + " grid=" + std::to_string(p->npanels);
       } else {
