@@ -155,6 +155,7 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   std::vector<int32_t> cols;
   std::vector<float> vals;
   int32_t max_pp = 0;
+  int64_t real_slots = 0, real_vals = 0;  // without the alignment padding
   for (int32_t q = 0; q < npanels; ++q) {
     panel_seg[(size_t)q] = (int32_t)seg.size();
     panel_slot[(size_t)q] = (int32_t)cols.size();
@@ -181,6 +182,13 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
       cols.insert(cols.end(), p.cb.begin() + a, p.cb.begin() + b);
       vals.insert(vals.end(), p.val32.begin() + (size_t)a * pop, p.val32.begin() + (size_t)b * pop);
     }
+    real_slots += (int64_t)cols.size() - panel_slot[(size_t)q];
+    real_vals += (int64_t)vals.size() - panel_val[(size_t)q];
+    // every panel's columns and values start on a 16-byte boundary, so a
+    // panel is staged with 16-byte loads; the padding (column 0, value 0)
+    // belongs to no segment and is never computed
+    while (cols.size() % 4) cols.push_back(0);
+    while (vals.size() % 4) vals.push_back(0.0f);
     max_pp = std::max(max_pp, (int32_t)cols.size() - panel_slot[(size_t)q]);
     max_pv = std::max(max_pv, (int32_t)vals.size() - panel_val[(size_t)q]);
   }
@@ -351,8 +359,8 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   plan->K = K;
   plan->km = km;
   plan->npanels = npanels;
-  plan->nslots = (int64_t)cols.size();
-  plan->nvals = (int64_t)vals.size();
+  plan->nslots = real_slots;
+  plan->nvals = real_vals;
   plan->nsegs = (int64_t)seg.size();
   plan->max_slots_per_panel = max_pp;
   plan->gen = gen;
