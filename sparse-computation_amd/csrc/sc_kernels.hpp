@@ -383,11 +383,14 @@ __global__ void __launch_bounds__(1024)
   const int LV = L * V;
   const int *cs = cols;
   const float *vs = vals;
+  // LDS: the cross-wave reduction area (W * KM * L * V floats), then the
+  // staged stream, so the reduction never overwrites the stream
+  const int red_floats = W > 1 ? W * KM * LV : 0;  // as sized by geometry()
   auto stage = [&]() {
     const int q0 = panel_val[panel];
     const int q1 = panel_val[panel + 1];
-    int *lc = reinterpret_cast<int *>(red);
-    float *lv = red + stage_cols;
+    int *lc = reinterpret_cast<int *>(red + red_floats);
+    float *lv = red + red_floats + stage_cols;
     stage_panel(lc, cols + p0, p1 - p0, lv, vals + q0, q1 - q0);
     __syncthreads();
     cs = lc - p0;  // indexed with global slot numbers
@@ -428,7 +431,6 @@ __global__ void __launch_bounds__(1024)
           if (row0 + r < M) store_c<V>(C + (size_t)(row0 + r) * N + c0, acc[r], accumulate);
       }
     } else {
-      if constexpr (STAGE) __syncthreads();  // every wave is done with the staged stream
       if (s == 0) {
 #pragma unroll
         for (int r = 0; r < KM; ++r)
@@ -448,10 +450,7 @@ __global__ void __launch_bounds__(1024)
           *dst = accumulate ? *dst + sum : sum;
         }
       }
-      __syncthreads();
-      if constexpr (STAGE) {
-        if (cbase + LV < N) stage();  // the reduction overwrote the stream
-      }
+      if (cbase + LV < N) __syncthreads();  // the next chunk reuses the reduction area
     }
   }
 }
@@ -1431,7 +1430,7 @@ inline Geometry geometry(int km, int N, int W, long long K = 0, int max_pslots =
     if (st <= kStageLimit) {
       g.stage = true;
       g.stage_cols = sc;
-      g.lds = st > red ? st : red;
+      g.lds = st + red;  // reduction area first, then the stream (panel_kernel)
     }
   }
   return g;
