@@ -41,31 +41,112 @@ def body_name(bits: str) -> str:
     return f"pattern_{bits}"
 
 
+def _narrow_loop(kn: int, unroll: int, step, indent="  "):
+    """Lanes-over-slots slot loop over the range [a.lo, a.hi) of a segment.
+
+    The segment's packs go to the S lane groups in one of two ways, chosen by
+    the argument type (A::kBlocked); either way group s gets q or q + 1 of
+    them (q = packs / S, the first `packs mod S` groups one more):
+
+    * blocked -- a contiguous block per group: the packs of a batch are
+      adjacent, so their columns and values sit at constant offsets from one
+      address;
+    * interleaved -- group s takes packs s, s + S, s + 2S, ... (adjacent lanes
+      read adjacent slots: one cache line for a read of columns from memory,
+      no LDS bank conflicts for one lane per slot).
+
+    Batches of `unroll` packs per group (their B loads all in flight), counted
+    the same for the whole wave, then one last batch of exactly the packs
+    left (1 .. unroll; a group with one pack fewer reads zeros for it), so a
+    segment costs ceil(packs / unroll) round trips and issues no load beyond
+    its longest group.  `step(u, masked, ind)` writes pack u of a batch (slot
+    j{u})."""
+    U = unroll
+    i2 = indent + "  "
+    i3 = indent + "    "
+    out = [f"{indent}const int np = (a.hi - a.lo) / {kn};",
+           f"{indent}const int sh = __builtin_ctz((unsigned)a.S);",
+           f"{indent}const int q = np >> sh;",
+           f"{indent}const int r = np & (a.S - 1);",
+           f"{indent}const int cnt = q + (a.s < r ? 1 : 0);",
+           f"{indent}const int jb = A::kBlocked ? a.lo + (a.s * q + min(a.s, r)) * {kn} : a.lo + a.s * {kn};",
+           f"{indent}const int stride = A::kBlocked ? {kn} : a.S * {kn};",
+           f"{indent}int b = 0;",
+           f"{indent}for (; b + {U} <= q; b += {U}) {{",
+           f"{i2}const int j = jb + b * stride;"]
+    for u in range(U):
+        out.append(f"{i2}const int j{u} = j + {u} * stride;")
+    for u in range(U):
+        out += step(u, False, i2)
+    out += [f"{indent}}}",
+            f"{indent}const int rem = q + (r > 0 ? 1 : 0) - b;  // 0 .. {U}",
+            f"{indent}if (rem > 0) {{",
+            f"{i2}const int j = jb + b * stride;"]
+    for t in range(1, U + 1):
+        if U == 1:
+            out.append(f"{i2}{{")
+        elif t == 1:
+            out.append(f"{i2}if (rem == 1) {{")
+        elif t < U:
+            out.append(f"{i2}}} else if (rem == {t}) {{")
+        else:
+            out.append(f"{i2}}} else {{")
+        for u in range(t):
+            out.append(f"{i3}const bool ok{u} = b + {u} < cnt;")
+            out.append(f"{i3}const int j{u} = ok{u} ? j + {u} * stride : a.lo;")
+        for u in range(t):
+            out += step(u, True, i3)
+    out.append(f"{i2}}}")
+    out.append(f"{indent}}}")
+    return out
+
+
+def _narrow_step(kn, pop, fmas):
+    """Pack u of a narrow batch: kn B-row loads and pop * kn values; a masked
+    pack (past the segment) loads a zero row and zero values."""
+    def step(u, masked, ind):
+        out = [f"{ind}const float *vp{u} = a.vals + a.vb + (j{u} - a.sb) * {pop};"]
+        for q in range(kn):
+            out.append(f"{ind}float b{u}_{q}[V];")
+            if masked:
+                out.append(f"{ind}sc::load_b_tail<V>(b{u}_{q}, a, a.cols[j{u} + {q}], ok{u});")
+            else:
+                out.append(f"{ind}sc::load_b<V>(b{u}_{q}, a, a.cols[j{u} + {q}]);")
+        # a masked pack's slot index is clamped into the segment, so its
+        # values are read unconditionally (no branch) and then cleared
+        def value(q):
+            def at(k):
+                e = f"vp{u}[{q * pop + k}]" if isinstance(k, int) else f"vp{u}[{q * pop} + {k}]"
+                return f"sc::keep_if(ok{u}, {e})" if masked else e
+            return at
+        return out, [(q, value(q)) for q in range(kn)]
+
+    def emit(u, masked, ind):
+        loads, vals = step(u, masked, ind)
+        return loads + fmas(u, vals, ind)
+    return emit
+
+
 def emit_body(km: int, bits: str, pid: int, kn: int, unroll: int) -> str:
     rows = _rows(bits)
     pop = len(rows)
     out = []
     out.append(f"// pattern id {pid}: bits {bits} -> panel rows {', '.join(map(str, rows))} "
-               f"(pop {pop}), packs of {kn} slot(s)")
+               f"(pop {pop}), packs of {kn} slot(s), {unroll} pack(s) per lane in flight")
     out.append("template <int V, class A>")
     out.append(f"__device__ __forceinline__ void {body_name(bits)}(float (&acc)[{km}][V], "
                "const A &a) {")
-    if unroll > 1:
-        out.append(f"#pragma unroll {unroll}")
-    out.append(f"  for (int j = a.lo + a.s * {kn}; j < a.hi; j += a.S * {kn}) {{")
-    out.append(f"    const float *vp = a.vals + a.vb + (j - a.sb) * {pop};")
-    for q in range(kn):
-        out.append(f"    const int c{q} = a.cols[j + {q}];")
-    for q in range(kn):
-        out.append(f"    float b{q}[V];")
-        out.append(f"    sc::load_b<V>(b{q}, a, c{q});")
-    for q in range(kn):
-        for k in range(pop):
-            out.append(f"    const float v{q}_{k} = vp[{q * pop + k}];")
-    for q in range(kn):
-        for k, r in enumerate(rows):
-            out.append(f"    sc::fma_row<V>(acc[{r}], v{q}_{k}, b{q});")
-    out.append("  }")
+
+    def fmas(u, vals, ind):
+        res = []
+        for q, value in vals:
+            for k in range(pop):
+                res.append(f"{ind}const float v{u}_{q}_{k} = {value(k)};")
+        for q, _ in vals:
+            for k, r in enumerate(rows):
+                res.append(f"{ind}sc::fma_row<V>(acc[{r}], v{u}_{q}_{k}, b{u}_{q});")
+        return res
+    out += _narrow_loop(kn, unroll, _narrow_step(kn, pop, fmas))
     out.append("}")
     return "\n".join(out)
 
@@ -253,11 +334,14 @@ def emit_pop_bodies(km: int, pop: int, kn: int, unroll: int, unroll_slots: int =
     out.append("template <int V, class A>")
     out.append(f"__device__ __forceinline__ void pop{pop}_narrow{head} {{")
     out += _mask_rows(km, "  ")
-    if unroll > 1:
-        out.append(f"#pragma unroll {unroll}")
-    out.append(f"  for (int j = a.lo + a.s * {kn}; j < a.hi; j += a.S * {kn}) {{")
-    out += _generic_step(km, pop, kn, "    ", "sc::load_b")
-    out.append("  }")
+
+    def fmas(u, vals, ind):
+        res = []
+        for q, value in vals:
+            for r in range(km):
+                res.append(f"{ind}if (h{r}) sc::fma_row<V>(acc[{r}], {value(f'k{r}')}, b{u}_{q});")
+        return res
+    out += _narrow_loop(kn, unroll, _narrow_step(kn, pop, fmas))
     out.append("}")
     # wave-wide slots
     U = kn * max(1, -(-unroll_slots // kn))

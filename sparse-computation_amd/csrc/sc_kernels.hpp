@@ -139,6 +139,16 @@ struct SegArgs {
   bool cval;                     // this lane's column group lies inside N
 };
 
+// Body arguments with the slot mapping of the pattern bodies fixed: blocked
+// (a lane group runs a contiguous block of a segment's slots, whose columns
+// and values sit at constant offsets from one LDS address) when the panel is
+// staged in LDS; interleaved when the bodies read columns and values from
+// memory, where the S lane groups' reads then share one cache line.
+template <class A, bool BLOCKED>
+struct Mapped : A {
+  static constexpr bool kBlocked = BLOCKED;
+};
+
 // Lanes whose column group lies past N read the last full group instead
 // (Bc clamped, always in bounds) and are never stored, so the loads need no
 // branch.
@@ -161,17 +171,21 @@ __device__ __forceinline__ void load_b(float (&b)[V], const SegArgs &a, int col)
 }
 
 // The same body arguments with B read through a buffer descriptor (B below
-// 4 GiB): the B-row address is one 32-bit multiply-add (row * N * 4 plus the
-// lane's column bytes), not 64-bit pointer arithmetic.
+// 2 GiB, K below 2^24): the B-row offset is one full-rate 24-bit
+// multiply-add (row * N * 4 plus the lane's column bytes), not 64-bit
+// pointer arithmetic.
 struct SegArgsBuf : SegArgs {
   __amdgpu_buffer_rsrc_t Bbuf;  // whole B
   unsigned voff;                // this lane's (clamped) column group, bytes
   unsigned row_bytes;           // N * 4
 };
 
+// A byte offset past every B the buffer path takes (B below 2 GiB): a buffer
+// load from it returns zeros without touching memory.
+constexpr unsigned kBufferOutOfRange = 0x80000000u;
+
 template <int V>
-__device__ __forceinline__ void load_b(float (&b)[V], const SegArgsBuf &a, int col) {
-  const unsigned off = (unsigned)col * a.row_bytes + a.voff;
+__device__ __forceinline__ void load_b_at(float (&b)[V], const SegArgsBuf &a, unsigned off) {
   if constexpr (V == 4) {
     const float4 t = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(a.Bbuf, off, 0, 0));
     b[0] = t.x;
@@ -184,6 +198,29 @@ __device__ __forceinline__ void load_b(float (&b)[V], const SegArgsBuf &a, int c
     b[1] = t.y;
   } else {
     b[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(a.Bbuf, off, 0, 0));
+  }
+}
+
+template <int V>
+__device__ __forceinline__ void load_b(float (&b)[V], const SegArgsBuf &a, int col) {
+  load_b_at<V>(b, a, __umul24((unsigned)col, a.row_bytes) + a.voff);
+}
+
+// load_b for the last batch of a segment's slot loop: a lane whose slot lies
+// past the segment (ok false; col is then a column in range) gets a zero row.
+// Through the buffer descriptor the load itself returns the zeros; the other
+// sources read the in-range row and clear it.
+template <int V, class A>
+__device__ __forceinline__ void load_b_tail(float (&b)[V], const A &a, int col, bool ok) {
+  if constexpr (std::is_base_of<SegArgsBuf, A>::value) {
+    // col is pinned (an empty asm) so that its read stays ahead of the
+    // select instead of moving into a branch of its own that waits on it
+    asm volatile("" : "+v"(col));
+    load_b_at<V>(b, a, ok ? __umul24((unsigned)col, a.row_bytes) + a.voff : kBufferOutOfRange);
+  } else {
+    load_b<V>(b, a, col);
+#pragma unroll
+    for (int e = 0; e < V; ++e) b[e] = ok ? b[e] : 0.f;
   }
 }
 
@@ -202,6 +239,7 @@ struct ChunkArgs {
   // sub-lanes per wave (V = 4: 8 lanes per slot); a compile-time constant so
   // that the bodies' slot loops need no division for their trip counts
   static constexpr int S = 64 / (kChunkCols / 4);
+  static constexpr bool kBlocked = false;  // slots interleaved over the lane groups
 };
 
 template <int V>
@@ -223,6 +261,10 @@ __device__ __forceinline__ void load_b(float (&b)[V], const ChunkArgs &a, int co
     b[0] = *p;
   }
 }
+
+// x if ok, else 0; x is an argument, so it is read whatever ok is (a select,
+// not a branch around the read).
+__device__ __forceinline__ float keep_if(bool ok, float x) { return ok ? x : 0.f; }
 
 template <int V>
 __device__ __forceinline__ void fma_row(float (&acc)[V], float v, const float (&b)[V]) {
@@ -400,7 +442,7 @@ __global__ void __launch_bounds__(1024)
   for (int cbase = 0; cbase < N; cbase += LV) {
     const int c0 = cbase + g * V;
     const int cl = min(c0, N - V);  // lanes past N read the last group, never stored
-    A args;
+    Mapped<A, STAGE> args;
     args.cols = cs;
     args.vals = vs;
     args.Bc = B + cl;
@@ -624,6 +666,9 @@ struct GatherArgs {
   int lo, hi;                      // slot range [lo, hi) of this wave in the segment
   int sb, vb;                      // first slot / first value of the segment
   int s, S;                        // slot sub-lane (the lane) and sub-lanes (64)
+  // slots interleaved over the lanes: adjacent lanes read adjacent gathered
+  // rows and values, free of LDS bank conflicts
+  static constexpr bool kBlocked = false;
 };
 
 template <int V>
@@ -1498,8 +1543,9 @@ hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int 
   hipLaunchKernelGGL((panel_kernel<KM, VV, ST, D, AA>), grid, block, g.lds, stream, v.seg, v.panel_seg,  \
                      v.panel_slot, v.panel_val, v.cols, v.vals, B, C, v.M, v.K, N, g.L, accumulate, pack, \
                      g.stage_cols)
-  // B below 4 GiB: byte offsets fit the buffer descriptor's 32 bits
-  const bool buf = (long long)v.K * N * (long long)sizeof(float) < (1ll << 31);
+  // B below 2 GiB: byte offsets stay inside the buffer descriptor's 31-bit
+  // range; K below 2^24: row numbers fit the 24-bit multiply
+  const bool buf = (long long)v.K * N * (long long)sizeof(float) < (1ll << 31) && v.K < (1 << 24);
   if (buf) {
     if (g.stage) {
       if (g.V == 4) SC_NARROW(4, true, SegArgsBuf);

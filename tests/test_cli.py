@@ -77,10 +77,15 @@ def test_main_spmm_emits_one_body_per_pattern(tmp_path, km, kn):
         assert f"void wide_{bits}(" in text
     assert f"sc_gen_spmm_km{km}_kn{kn}_record = {{{km}, {kn}, 0, {2 ** km - 1}, 0," in text
     assert f"sc_gen_spmm_km{km}_kn{kn}_launch" in text
-    # a pack of kn slots is unrolled: kn B-row loads per step in the narrow body
+    # a pack of kn slots is unrolled, U = max(1, 4 // kn) packs per batch: a
+    # full batch of U * kn B-row loads, then a last batch of exactly the t
+    # packs left (t = 1 .. U; t * kn loads that may read zeros)
+    U = max(1, 4 // kn)
     body = text.split(f"void pattern_{'1' * km}(")[1].split("\n}\n")[0]
-    assert body.count("sc::load_b<V>") == kn
-    assert body.count("sc::fma_row<V>") == kn * km
+    tail = U * (U + 1) // 2
+    assert body.count("sc::load_b<V>") == U * kn
+    assert body.count("sc::load_b_tail<V>") == tail * kn
+    assert body.count("sc::fma_row<V>") == (U + tail) * kn * km
 
 
 def test_main_spmm_dictionary_and_dense(tmp_path):
