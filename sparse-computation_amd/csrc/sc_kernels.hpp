@@ -773,48 +773,63 @@ __device__ __forceinline__ void gather_rows(typename VecOf<V>::T *dst, const int
   }
 }
 
-// The fp32 small-N staging in one pipeline: the panel's values and column
-// indices are loaded together, the B rows as soon as the columns arrive (the
-// values still in flight), then everything is stored to LDS.
-template <int V, int UC, int UV>
+// The fp32 small-N staging in one pipeline, with 16-byte loads: a panel's
+// columns and values start on 16-byte boundaries and are padded to multiples
+// of 4 (column 0, value 0), so a thread loads groups of four columns (one
+// int4) and four values (one float4), gathers the four B rows as soon as the
+// columns arrive (the values still in flight), then stores everything to LDS.
+// U groups of each per thread are in flight.
+template <int V, int U>
 __device__ __forceinline__ void stage_values_gather_rows(float *lv, const float *__restrict__ vals, int nv,
                                                          typename VecOf<V>::T *gb, const int *__restrict__ cols,
                                                          const void *__restrict__ B, int nc) {
   using T = typename VecOf<V>::T;
   const T *Bv = reinterpret_cast<const T *>(B);
+  const vec4i *c4 = reinterpret_cast<const vec4i *>(cols);
+  const vec4f *v4 = reinterpret_cast<const vec4f *>(vals);
+  vec4f *l4 = reinterpret_cast<vec4f *>(lv);
+  const int nc4 = nc / 4;
+  const int nv4 = nv / 4;
   const int step = blockDim.x;
-  for (int pass = 0;; ++pass) {
-    const int bc = threadIdx.x + pass * step * UC;
-    const int bv = threadIdx.x + pass * step * UV;
-    if (bc >= nc && bv >= nv) break;
-    int c[UC];
-    float v[UV];
-    T r[UC];
-    if (nc > 0) {
+  for (int base = threadIdx.x; base < nc4 || base < nv4; base += step * U) {
+    vec4i c[U];
+    vec4f v[U];
+    T r[U][4];
+    if (nc4 > 0) {
 #pragma unroll
-      for (int u = 0; u < UC; ++u) c[u] = __builtin_nontemporal_load(&cols[min(bc + u * step, nc - 1)]);
+      for (int u = 0; u < U; ++u) c[u] = __builtin_nontemporal_load(&c4[min(base + u * step, nc4 - 1)]);
     }
-    if (nv > 0) {
+    if (nv4 > 0) {
 #pragma unroll
-      for (int u = 0; u < UV; ++u) v[u] = __builtin_nontemporal_load(&vals[min(bv + u * step, nv - 1)]);
+      for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(&v4[min(base + u * step, nv4 - 1)]);
     }
-    if (nc > 0) {
+    if (nc4 > 0) {
 #pragma unroll
-      for (int u = 0; u < UC; ++u) keep(c[u]);
+      for (int u = 0; u < U; ++u) keep(c[u]);
 #pragma unroll
-      for (int u = 0; u < UC; ++u) r[u] = Bv[c[u]];
+      for (int u = 0; u < U; ++u) {
+        r[u][0] = Bv[c[u].x];
+        r[u][1] = Bv[c[u].y];
+        r[u][2] = Bv[c[u].z];
+        r[u][3] = Bv[c[u].w];
+      }
 #pragma unroll
-      for (int u = 0; u < UC; ++u) keep(r[u]);
+      for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int u = 0; u < UC; ++u)
-        if (bc + u * step < nc) gb[bc + u * step] = r[u];
+        for (int e = 0; e < 4; ++e) keep(r[u][e]);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (base + u * step < nc4) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) gb[(base + u * step) * 4 + e] = r[u][e];
+        }
     }
-    if (nv > 0) {
+    if (nv4 > 0) {
 #pragma unroll
-      for (int u = 0; u < UV; ++u) keep(v[u]);
+      for (int u = 0; u < U; ++u) keep(v[u]);
 #pragma unroll
-      for (int u = 0; u < UV; ++u)
-        if (bv + u * step < nv) lv[bv + u * step] = v[u];
+      for (int u = 0; u < U; ++u)
+        if (base + u * step < nv4) l4[base + u * step] = v[u];
     }
   }
 }
@@ -880,7 +895,7 @@ __global__ void __launch_bounds__(1024)
     stage_half_values<8>(lv, reinterpret_cast<const unsigned short *>(vals) + q0, q1 - q0);
     gather_rows<V, 8, HALF>(reinterpret_cast<typename VecOf<V>::T *>(gb), cols + p0, B, p1 - p0);
   } else {
-    stage_values_gather_rows<V, 8, 8>(lv, reinterpret_cast<const float *>(vals) + q0, q1 - q0,
+    stage_values_gather_rows<V, 2>(lv, reinterpret_cast<const float *>(vals) + q0, q1 - q0,
                                       reinterpret_cast<typename VecOf<V>::T *>(gb), cols + p0, B, p1 - p0);
   }
   __syncthreads();
