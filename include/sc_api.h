@@ -120,6 +120,14 @@ void sc_cfmtx_free(sc_cfmtx *cf);
 #define SC_PLAN_CHUNKED 4      /* build the K-block-major copy of the chunk kernel
                                   (B column chunks resident in LDS, N % 32 == 0)   */
 #define SC_PLAN_F16_VALUES 8   /* also keep a binary16 copy of the values (sc_spmm_f16) */
+#define SC_PLAN_ROWS 16        /* lay the slots out as one-row panels (kernel_m 1):
+                                  one workgroup per row instead of per km rows  */
+#define SC_PLAN_PATTERNS 32    /* keep only the km-row pattern layout           */
+/* Without SC_PLAN_ROWS, SC_PLAN_PATTERNS, SC_PLAN_TILED or SC_PLAN_CHUNKED a
+ * plan of a kernel_m > 1 file holds both layouts, and sc_spmm / sc_spmv run
+ * the one-row layout while its B-row gathers (4 * stored entries * N bytes)
+ * total under 128 MiB, the km-row pattern layout above.  sc_spmm_generated
+ * and sc_spmm_f16 always run the pattern layout. */
 
 /* allocateAndCopyMixedFormat (example_cuda/spmm_demo_gpu_utils.h:207-245) and
  * the constructors of the generated classes SpMMMixePatternGeneralCacheLess /

@@ -73,6 +73,12 @@ struct sc_plan {
   int32_t max_slots_per_panel = 0;
   int32_t kn = 0;            // column pack of the .cfmtx header
   bool dropped_pad = false;  // padding slots omitted on the device
+  int32_t rows_of_km = 0;    // a one-row layout of a kernel_m > 1 file: that kernel_m
+  // The same slots as one-row panels (rows_of), owned by this plan; launches
+  // whose B-row gathers in that layout stay small run on it (layout_for).
+  // Null with SC_PLAN_ROWS, SC_PLAN_PATTERNS, SC_PLAN_TILED, SC_PLAN_CHUNKED
+  // and for kernel_m 1.
+  sc_plan *rows = nullptr;
   std::vector<uint32_t> masks;  // row masks of the patterns holding slots
   void *dmem = nullptr;  // one allocation holding every array
   // split-K partial sums of the tiled kernel: grown on the first call that
@@ -94,22 +100,21 @@ size_t align_up(size_t off) {
   return (off + 255) / 256 * 256;
 }
 
-sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
+struct PatInfo {
+  uint32_t mask;
+  int pop;
+};
+
+// Validate every pattern block against the header so no kernel can read
+// outside the plan or write outside C; returns each block's row mask and pop.
+std::vector<PatInfo> validate(const sc::Cfmtx &cf) {
   if (cf.km < 1) throw sc::Error{SC_ERR_FORMAT, "kernel_m must be >= 1"};
   if (cf.km > kMaxBuiltinKm)
     throw sc::Error{SC_ERR_UNSUPPORTED, "no pattern kernels built for kernel_m " + std::to_string(cf.km) +
                                             " (1.." + std::to_string(kMaxBuiltinKm) + ")"};
-  const int32_t km = cf.km, M = cf.m, K = cf.n, npanels = cf.npanels();
-  const bool drop_pad = (flags & SC_PLAN_DROP_PADDING) != 0;
+  const int32_t km = cf.km, K = cf.n, npanels = cf.npanels();
   const GenEntry gen = kBuiltin[km];
   std::vector<uint32_t> supported(gen.rec->masks, gen.rec->masks + gen.rec->npatterns);
-
-  // validate every pattern block against the header so no kernel can read
-  // outside the plan or write outside C
-  struct PatInfo {
-    uint32_t mask;
-    int pop;
-  };
   std::vector<PatInfo> info(cf.patterns.size());
   for (size_t i = 0; i < cf.patterns.size(); ++i) {
     const sc::Pattern &p = cf.patterns[i];
@@ -141,6 +146,127 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
     if (std::find(supported.begin(), supported.end(), mask) == supported.end())
       throw sc::Error{SC_ERR_UNSUPPORTED, "no kernel body for pattern " + p.bits};
   }
+  return info;
+}
+
+// End of slot range [a, b) of a segment without its trailing padding: the
+// builder pads a segment to a multiple of kernel_n by repeating its last
+// column with all-zero values (code_gen/ss_format/format_generator.py:48-63).
+int32_t unpadded_end(const sc::Pattern &p, int pop, int32_t a, int32_t b) {
+  while (b - 1 > a && p.cb[(size_t)b - 1] == p.cb[(size_t)b - 2]) {
+    for (int k = 0; k < pop; ++k) {
+      const float v = p.val32[(size_t)(b - 1) * pop + k];
+      if (v != 0.0f || std::signbit(v)) return b;
+    }
+    --b;
+  }
+  return b;
+}
+
+// The same slots re-laid as one-row panels (kernel_m 1): row q*km + r holds,
+// in ascending column order, every slot of panel q whose pattern contains
+// row r, with that row's value.  The file's coarsening decides which values
+// sit together; this layout gives each row its own workgroup, four to six
+// times the workgroups of a km = 4..6 plan on the same matrix.
+sc::Cfmtx rows_of(const sc::Cfmtx &cf, const std::vector<PatInfo> &info, bool drop_pad) {
+  const int32_t km = cf.km, M = cf.m, npanels = cf.npanels();
+  sc::Cfmtx r;
+  r.m = M;
+  r.n = cf.n;
+  r.km = 1;
+  r.kn = 1;
+  r.kind = cf.kind;
+  r.header_order = {0};
+  sc::Pattern rp;
+  rp.bits = "1";
+  rp.id = 0;
+  rp.pop = 1;
+  rp.rpp.assign((size_t)M + 1, 0);
+  auto each_entry = [&](auto &&fn) {
+    for (size_t i = 0; i < cf.patterns.size(); ++i) {
+      const sc::Pattern &p = cf.patterns[i];
+      const int pop = info[i].pop;
+      if (pop == 0) continue;
+      int rows[32], nr = 0;
+      for (int b = 0; b < km; ++b)
+        if (info[i].mask >> b & 1u) rows[nr++] = b;
+      for (int32_t q = 0; q < npanels; ++q) {
+        const int32_t a = p.rpp[(size_t)q];
+        const int32_t e = drop_pad ? unpadded_end(p, pop, a, p.rpp[(size_t)q + 1]) : p.rpp[(size_t)q + 1];
+        for (int k = 0; k < nr; ++k) {
+          const int32_t row = q * km + rows[k];
+          if (row >= M) continue;  // rows of the last panel past the matrix hold only zeros
+          for (int32_t j = a; j < e; ++j) fn(row, p.cb[(size_t)j], p.val32[(size_t)j * pop + k]);
+        }
+      }
+    }
+  };
+  each_entry([&](int32_t row, int32_t, float) { ++rp.rpp[(size_t)row + 1]; });
+  for (int32_t i = 0; i < M; ++i) {
+    rp.rpp[(size_t)i + 1] += rp.rpp[(size_t)i];
+    if (rp.rpp[(size_t)i + 1] < 0) throw sc::Error{SC_ERR_UNSUPPORTED, "plan larger than int32 offsets"};
+  }
+  const size_t n = (size_t)rp.rpp[(size_t)M];
+  std::vector<std::pair<int32_t, float>> ent(n);
+  std::vector<int32_t> fill(rp.rpp.begin(), rp.rpp.end() - 1);
+  each_entry([&](int32_t row, int32_t c, float v) { ent[(size_t)fill[(size_t)row]++] = {c, v}; });
+  rp.cb.resize(n);
+  rp.val32.resize(n);
+  for (int32_t i = 0; i < M; ++i) {
+    auto b = ent.begin() + rp.rpp[(size_t)i], e = ent.begin() + rp.rpp[(size_t)i + 1];
+    std::stable_sort(b, e, [](const auto &x, const auto &y) { return x.first < y.first; });
+  }
+  for (size_t j = 0; j < n; ++j) {
+    rp.cb[j] = ent[j].first;
+    rp.val32[j] = ent[j].second;
+  }
+  r.patterns.push_back(std::move(rp));
+  return r;
+}
+
+sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags);
+
+// SC_PLAN_ROWS: a km = 1 plan of the same slots (rows_of); a km = 1 file
+// already is one.
+sc_plan *create_rows_plan(const sc::Cfmtx &cf, int32_t flags) {
+  const std::vector<PatInfo> info = validate(cf);
+  if (cf.km == 1) return create_plan(cf, flags & ~SC_PLAN_ROWS);
+  sc_plan *p = create_plan(rows_of(cf, info, (flags & SC_PLAN_DROP_PADDING) != 0), flags & ~SC_PLAN_ROWS);
+  p->rows_of_km = cf.km;
+  return p;
+}
+
+sc_plan *build_plan(const sc::Cfmtx &cf, int32_t flags, const std::vector<PatInfo> &info);
+
+sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
+  if (flags & SC_PLAN_ROWS) return create_rows_plan(cf, flags);
+  const std::vector<PatInfo> info = validate(cf);
+  std::unique_ptr<sc_plan, void (*)(sc_plan *)> plan(build_plan(cf, flags, info), sc_plan_destroy);
+  if (cf.km > 1 && !(flags & (SC_PLAN_PATTERNS | SC_PLAN_TILED | SC_PLAN_CHUNKED))) {
+    plan->rows = create_plan(rows_of(cf, info, (flags & SC_PLAN_DROP_PADDING) != 0), flags & SC_PLAN_DROP_PADDING);
+    plan->rows->rows_of_km = cf.km;
+  }
+  return plan.release();
+}
+
+// The layout a launch at N columns runs on.  The one-row layout gathers one
+// B row per stored entry and runs one workgroup per row; the km-row panels
+// gather one B row per slot (pop rows share it) with km times fewer, longer
+// workgroups.  While the one-row layout's gathers total under 128 MiB the
+// launch is bound by the panels' dependent chains, not by gathered bytes, and
+// the one-row layout wins: measured on MI355X 1.1-3.8x on 512x512 at km 2..6
+// and N = 1..128 and on 2048x512 / 512x2048 at 80-98 % sparsity, N = 128.
+// Above it the panels' B-row reuse wins: 1.1-1.5x on 4096x4096 structured at
+// N = 32, 128 and 2048x512 at 50-70 %.
+const sc_plan *layout_for(const sc_plan *p, int N) {
+  if (p->rows && 4.0 * (double)p->rows->view.nslots * N < 134217728.0) return p->rows;
+  return p;
+}
+
+sc_plan *build_plan(const sc::Cfmtx &cf, int32_t flags, const std::vector<PatInfo> &info) {
+  const int32_t km = cf.km, M = cf.m, K = cf.n, npanels = cf.npanels();
+  const bool drop_pad = (flags & SC_PLAN_DROP_PADDING) != 0;
+  const GenEntry gen = kBuiltin[km];
 
   // flatten panel-major, a panel's segments in descending row-mask order: the
   // generated dispatchers visit the patterns in that fixed order
@@ -165,17 +291,7 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
       const int pop = info[i].pop;
       int32_t a = p.rpp[(size_t)q], b = p.rpp[(size_t)q + 1];
       if (b <= a) continue;
-      if (drop_pad) {
-        // trailing padding: repeated last column with all-zero values
-        while (b - 1 > a && p.cb[(size_t)b - 1] == p.cb[(size_t)b - 2]) {
-          bool zero = true;
-          for (int k = 0; k < pop; ++k)
-            if (p.val32[(size_t)(b - 1) * pop + k] != 0.0f || std::signbit(p.val32[(size_t)(b - 1) * pop + k]))
-              zero = false;
-          if (!zero) break;
-          --b;
-        }
-      }
+      if (drop_pad) b = unpadded_end(p, pop, a, b);
       if ((int64_t)cols.size() + (b - a) > INT32_MAX || (int64_t)vals.size() + (int64_t)(b - a) * pop > INT32_MAX)
         throw sc::Error{SC_ERR_UNSUPPORTED, "plan larger than int32 offsets"};
       seg.push_back(make_int4((int)info[i].mask, (int)cols.size(), b - a, (int)vals.size()));
@@ -558,8 +674,11 @@ extern "C" {
 int sc_plan_create(const sc_cfmtx *cf, int32_t flags, sc_plan **out) {
   SC_GUARD([&] {
     if (!cf || !out) throw sc::Error{SC_ERR_ARG, "null argument"};
-    if (flags & ~(SC_PLAN_DROP_PADDING | SC_PLAN_TILED | SC_PLAN_CHUNKED | SC_PLAN_F16_VALUES))
+    if (flags & ~(SC_PLAN_DROP_PADDING | SC_PLAN_TILED | SC_PLAN_CHUNKED | SC_PLAN_F16_VALUES | SC_PLAN_ROWS |
+                  SC_PLAN_PATTERNS))
       throw sc::Error{SC_ERR_ARG, "unknown plan flags"};
+    if ((flags & SC_PLAN_ROWS) && (flags & SC_PLAN_PATTERNS))
+      throw sc::Error{SC_ERR_ARG, "SC_PLAN_ROWS and SC_PLAN_PATTERNS are exclusive"};
     if ((flags & SC_PLAN_TILED) && (flags & SC_PLAN_CHUNKED))
       throw sc::Error{SC_ERR_ARG, "SC_PLAN_TILED and SC_PLAN_CHUNKED are exclusive"};
     *out = create_plan(sc_cfmtx_ref(cf), flags);
@@ -584,6 +703,7 @@ int sc_plan_describe(const sc_plan *p, int32_t N, char *buf, size_t buflen) {
   SC_GUARD([&] {
     if (!p || !buf || buflen == 0) throw sc::Error{SC_ERR_ARG, "null argument"};
     if (N < 1) throw sc::Error{SC_ERR_ARG, "N must be >= 1"};
+    p = layout_for(p, N);
     std::string d;
     const sc::TileGeometry tg = sc::tile_geometry(p->view, N);
     const sc::ChunkGeometry cg = sc::chunk_geometry(p->view, N);
@@ -610,6 +730,7 @@ int sc_plan_describe(const sc_plan *p, int32_t N, char *buf, size_t buflen) {
             std::to_string(g.stage ? 1 : 0) + " waves=" + std::to_string(w) + " grid=" + std::to_string(p->npanels);
       }
     }
+    if (p->rows_of_km > 1) d += " (rows of km=" + std::to_string(p->rows_of_km) + ")";
     if (d.size() + 1 > buflen) throw sc::Error{SC_ERR_ARG, "buffer too small"};
     std::memcpy(buf, d.c_str(), d.size() + 1);
   });
@@ -620,6 +741,7 @@ int sc_spmm(const sc_plan *plan, const float *dB, float *dC, int32_t N, int32_t 
   SC_GUARD([&] {
     if (flags & ~SC_ACCUMULATE) throw sc::Error{SC_ERR_ARG, "unknown flags"};
     if (!plan) throw sc::Error{SC_ERR_ARG, "null plan"};
+    if (N >= 1) plan = layout_for(plan, N);
     launch(plan, plan->gen.rec, (sc_gen_launch_fn)plan->gen.launch, dB, dC, N, flags, waves_per_panel, hip_stream);
   });
 }
@@ -636,6 +758,7 @@ int sc_spmv(const sc_plan *plan, const float *dx, float *dy, int32_t flags, void
   SC_GUARD([&] {
     if (flags & ~SC_ACCUMULATE) throw sc::Error{SC_ERR_ARG, "unknown flags"};
     if (!plan) throw sc::Error{SC_ERR_ARG, "null plan"};
+    plan = layout_for(plan, 1);
     launch(plan, plan->gen.rec, (sc_gen_launch_fn)plan->gen.launch, dx, dy, 1, flags, 0, hip_stream);
   });
 }
@@ -667,6 +790,7 @@ int sc_spmm_f16(const sc_plan *plan, const void *dB, void *dC, int32_t N, int32_
 
 void sc_plan_destroy(sc_plan *plan) {
   if (!plan) return;
+  sc_plan_destroy(plan->rows);
   if (plan->dmem) (void)hipFree(plan->dmem);
   if (plan->work) (void)hipFree(plan->work);
   if (plan->tcount) (void)hipFree(plan->tcount);

@@ -2,8 +2,9 @@
 // gfx950: random 512-byte row gathers from an L2-resident table (the B-row
 // gathers of the wide kernel), contiguous streaming reads from L2, the
 // strided K x Nc column-chunk reads that stage a B chunk in LDS, LDS read
-// bandwidth (b64/b128), LDS b128 reads of random rows (lanes over slots) and
-// L1-hit reads.
+// bandwidth (b64/b128), LDS b128 reads of random rows (lanes over slots),
+// L1-hit reads, and the issue rate of the fp32 MFMA shapes a km = 4 slot
+// maps to (v_mfma_f32_4x4x1f32: one 4x1 column block times 64 columns of B).
 // All indices are masked into their buffers; every loop has a fixed trip count.
 //   hipcc --offload-arch=gfx950 -O3 -Xclang -target-feature -Xclang -packed-fp32-ops \
 //         ubench_memory.hip -o ../../lib/ubench_memory
@@ -157,6 +158,29 @@ __global__ void l1_read(const float4 *__restrict__ buf, int iters, float *out) {
   if (acc == 1234.5f) out[0] = acc;
 }
 
+// fp32 MFMA issue rate: 8 independent accumulator chains per wave, `iters`
+// steps each.  KIND 0: v_mfma_f32_4x4x1f32 (16 blocks of 4x4x1), KIND 1:
+// v_mfma_f32_16x16x4f32.
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+template <int KIND>
+__global__ void __launch_bounds__(256) mfma_rate(float a, float b, int iters, float *out) {
+  v4f_t acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = (v4f_t){0.f, 0.f, 0.f, 0.f};
+  const float x = a + (float)threadIdx.x;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (KIND == 0) acc[i] = __builtin_amdgcn_mfma_f32_4x4x1f32(x, b, acc[i], 0, 0, 0);
+      else acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, b, acc[i], 0, 0, 0);
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s += acc[i][0] + acc[i][1] + acc[i][2] + acc[i][3];
+  if (s == 1234.5f) out[0] = s;
+}
+
 int main() {
   hipDeviceProp_t prop;
   CK(hipGetDeviceProperties(&prop, 0));
@@ -302,6 +326,26 @@ int main() {
     double bytes = 10.0 * blocks * wpb * iters * 8 * 1024.0;
     printf("l1 read dwordx4: %.2f TB/s (%.1f B/clk/CU)\n", bytes / (ms * 1e-3) / 1e12,
            bytes / (ms * 1e-3) / CUs / (prop.clockRate * 1e3));
+  }
+  {
+    // 4 waves per SIMD; cycles per MFMA per SIMD at the reported clock
+    const int blocks = 4 * CUs, iters = 2000;
+    for (int kind = 0; kind < 2; ++kind) {
+      float ms = 0.f;
+      for (int rep = 0; rep < 2; ++rep) {  // first launch warms up
+        CK(hipEventRecord(e0));
+        if (kind == 0) hipLaunchKernelGGL(mfma_rate<0>, dim3(blocks), dim3(256), 0, 0, 1.f, 2.f, iters, out);
+        else hipLaunchKernelGGL(mfma_rate<1>, dim3(blocks), dim3(256), 0, 0, 1.f, 2.f, iters, out);
+        CK(hipEventRecord(e1));
+        CK(hipEventSynchronize(e1));
+        CK(hipEventElapsedTime(&ms, e0, e1));
+      }
+      const double per_simd = (double)blocks * 4 * iters * 8 / (4.0 * CUs);
+      const double fmas = kind == 0 ? 256.0 : 1024.0;
+      printf("mfma %s: %.1f cycles per instruction per SIMD, %.1f fp32 TFLOP/s\n",
+             kind == 0 ? "f32_4x4x1 (16 blocks)" : "f32_16x16x4", ms * 1e-3 * prop.clockRate * 1e3 / per_simd,
+             2.0 * fmas * per_simd * 4 * CUs / (ms * 1e-3) / 1e12);
+    }
   }
   return 0;
 }

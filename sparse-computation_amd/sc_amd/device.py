@@ -13,6 +13,8 @@ PLAN_DROP_PADDING = 1
 PLAN_TILED = 2
 PLAN_CHUNKED = 4
 PLAN_F16_VALUES = 8
+PLAN_ROWS = 16
+PLAN_PATTERNS = 32
 ACCUMULATE = 1
 
 

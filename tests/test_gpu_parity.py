@@ -21,11 +21,14 @@ torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda:0"
+# the km-row pattern layout only: these tests cover the pattern kernels (the
+# one-row layout that default plans also hold is covered in test_gpu_rows.py)
+PAT = sc_amd.PLAN_PATTERNS
 
 
 def run_spmm(A, B, km, kn, flags=0, waves=0, accumulate=None):
     cf = sc_amd.Cfmtx.build(A, km, kn)
-    plan = sc_amd.Plan(cf, flags)
+    plan = sc_amd.Plan(cf, flags | sc_amd.PLAN_PATTERNS)
     Bt = torch.from_numpy(np.ascontiguousarray(B, np.float32)).to(DEV)
     if accumulate is not None:
         Ct = torch.from_numpy(accumulate.copy()).to(DEV)
@@ -111,7 +114,8 @@ def test_spmm_drop_padding_plan():
     # tolerance, and the plan must hold fewer slots.
     A, B = synth_case(512, 512, 0.2, 64, seed=21)
     cf = sc_amd.Cfmtx.build(A, 4, 8)
-    assert sc_amd.Plan(cf, sc_amd.PLAN_DROP_PADDING).info()["nslots"] < sc_amd.Plan(cf).info()["nslots"]
+    assert (sc_amd.Plan(cf, sc_amd.PLAN_DROP_PADDING | PAT).info()["nslots"]
+            < sc_amd.Plan(cf, PAT).info()["nslots"])
     C1 = run_spmm(A, B, 4, 8)
     C2 = run_spmm(A, B, 4, 8, flags=sc_amd.PLAN_DROP_PADDING)
     assert oracle_check(A, B, C1)[0] <= REL_TOL
@@ -149,7 +153,7 @@ def test_fixture_matrix_bit_exact(km, kn):
 def test_spmv_matches_reference_cpu_path():
     A, B = synth_case(512, 512, 0.30, 1, seed=0x5EED0000 + 0)
     cf = sc_amd.Cfmtx.build(A, 1, 1)
-    plan = sc_amd.Plan(cf)
+    plan = sc_amd.Plan(cf, PAT)
     x = torch.from_numpy(B[:, 0].copy()).to(DEV)
     y = plan.spmv(x)
     torch.cuda.synchronize()
@@ -163,7 +167,7 @@ def test_spmv_matches_reference_cpu_path():
 
 def test_plan_rejects_bad_device_buffer_shapes():
     A, B = synth_case(64, 64, 0.2, 4, seed=1)
-    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1))
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1), PAT)
     with pytest.raises(ValueError):
         plan.spmm(torch.zeros((63, 4), device=DEV))
 
@@ -178,7 +182,7 @@ def test_spmm_b_above_2_gib(n):
     A = sc_amd.Csr.synth_uniform(64, K, 3000 / (64 * K), 0.05, 0x5EED0000 + 9800 + n)
     gen = torch.Generator(device=DEV).manual_seed(n)
     Bt = torch.empty((K, n), dtype=torch.float32, device=DEV).uniform_(-1.0, 1.0, generator=gen)
-    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1))
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1), PAT)
     assert plan.describe(n).startswith("panel_kernel")
     C = plan.spmm(Bt)
     torch.cuda.synchronize()
@@ -238,7 +242,7 @@ def test_tiled_split_k_back_to_back_inputs(n):
 def test_spmm_is_deterministic(flags):
     A, B = synth_case(4096, 4096, 0.10, 128, seed=77, structured=True)
     cf = sc_amd.Cfmtx.build(A, 4, 1)
-    plan = sc_amd.Plan(cf, flags)
+    plan = sc_amd.Plan(cf, flags | sc_amd.PLAN_PATTERNS)
     Bt = torch.from_numpy(B).to(DEV)
     C1 = plan.spmm(Bt).cpu().numpy()
     C2 = plan.spmm(Bt).cpu().numpy()
@@ -306,7 +310,7 @@ def test_small_n_gather_kernel(n, waves):
     # N = 1, 2, 4: B rows of the panel gathered into LDS before the pattern
     # bodies run; ragged M, several waves per panel, accumulate
     A, B = synth_case(515, 700, 0.15, n, seed=0x5EED0000 + 9800 + n * 20 + waves)
-    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 2))
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 2), PAT)
     assert plan.describe(n).startswith("gather_kernel")
     C = run_spmm(A, B, 4, 2, waves=waves)
     assert oracle_check(A, B, C)[0] <= REL_TOL
@@ -323,7 +327,7 @@ def test_small_n_gather_kernel_generated_pack_unit(n):
     unit = sc_amd.GeneratedUnit(os.path.join(os.path.dirname(sc_amd.LIB_PATH), "units",
                                              "libsc_unit_spmm_km4_kn2.so"), "spmm_km4_kn2")
     A, B = synth_case(256, 300, 0.2, n, seed=0x5EED0000 + 9900 + n)
-    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 2))
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 2), PAT)
     C = plan.spmm_generated(unit, torch.from_numpy(B).to(DEV))
     torch.cuda.synchronize()
     assert oracle_check(A, B, C.cpu().numpy())[0] <= REL_TOL

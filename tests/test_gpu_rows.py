@@ -1,0 +1,137 @@
+"""GPU parity of SC_PLAN_ROWS plans: a km > 1 .cfmtx re-laid on the device as
+one-row panels (kernel_m 1), against the CPU oracle on the same inputs.
+
+Floating point: max relative error <= 1e-5 normalised by (|A| |B|)_ij
+against the fp64 product of the same fp32 operands; integer-valued inputs
+must come out exact.
+"""
+import numpy as np
+import pytest
+
+import sc_amd
+from cases import REL_TOL, oracle_check, synth_case
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def run(A, B, km, kn, flags=sc_amd.PLAN_ROWS, accumulate=None):
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, km, kn), flags)
+    Bt = torch.from_numpy(np.ascontiguousarray(B, np.float32)).to(DEV)
+    if accumulate is not None:
+        Ct = torch.from_numpy(accumulate.copy()).to(DEV)
+        plan.spmm(Bt, Ct, accumulate=True)
+    else:
+        Ct = torch.full((A.shape[0], B.shape[1]), float("nan"), device=DEV)  # must be overwritten
+        plan.spmm(Bt, Ct)
+    torch.cuda.synchronize()
+    return plan, Ct.cpu().numpy()
+
+
+@pytest.mark.parametrize("n", [1, 2, 4, 32, 128])
+@pytest.mark.parametrize("km", [2, 3, 4, 5, 6])
+def test_rows_plan_512(km, n):
+    A, B = synth_case(512, 512, 0.20, n, seed=0x5EED0000 + 1000 + km * 10 + n)
+    plan, C = run(A, B, km, 2)
+    err, _ = oracle_check(A, B, C)
+    assert err <= REL_TOL, (km, n, err)
+    assert plan.info()["km"] == 1
+    assert f"(rows of km={km})" in plan.describe(n)
+
+
+@pytest.mark.parametrize("kn", [1, 3, 8, 0])
+@pytest.mark.parametrize("drop", [0, sc_amd.PLAN_DROP_PADDING])
+def test_rows_plan_column_packs(kn, drop):
+    A, B = synth_case(256, 320, 0.15, 4, seed=0x5EED0000 + 9100 + kn)
+    plan, C = run(A, B, 4, kn, sc_amd.PLAN_ROWS | drop)
+    err, _ = oracle_check(A, B, C)
+    assert err <= REL_TOL, (kn, drop, err)
+    if drop:
+        # every padding slot is gone: one slot per stored entry
+        assert plan.info()["nslots"] == A.nnz
+
+
+def test_rows_plan_ragged_and_empty_rows():
+    # 37 rows (the last panel of km 4, 5, 6 is partial), rows 5..12 and the
+    # last row empty
+    rng = np.random.default_rng(11)
+    dense = (rng.random((37, 53)) < 0.3) * rng.standard_normal((37, 53))
+    dense[5:13] = 0
+    dense[-1] = 0
+    ip = np.concatenate([[0], np.cumsum((dense != 0).sum(1))]).astype(np.int32)
+    ix = np.nonzero(dense)[1].astype(np.int32)
+    dx = dense[dense != 0].astype(np.float32).astype(np.float64)
+    A = sc_amd.Csr.from_arrays(37, 53, ip, ix, dx)
+    B = sc_amd.synth_dense(53 * 8, 78).reshape(53, 8)
+    for km in (3, 4, 5, 6):
+        _, C = run(A, B, km, 2)
+        err, _ = oracle_check(A, B, C)
+        assert err <= REL_TOL, (km, err)
+        assert np.all(C[5:13] == 0) and np.all(C[-1] == 0)
+
+
+def test_rows_plan_integer_inputs_are_exact():
+    # small-integer A and B: every partial sum is exact in fp32
+    rng = np.random.default_rng(12)
+    dense = (rng.random((200, 300)) < 0.2) * rng.integers(-3, 4, (200, 300))
+    ip = np.concatenate([[0], np.cumsum((dense != 0).sum(1))]).astype(np.int32)
+    ix = np.nonzero(dense)[1].astype(np.int32)
+    dx = dense[dense != 0].astype(np.float64)
+    A = sc_amd.Csr.from_arrays(200, 300, ip, ix, dx)
+    B = rng.integers(-4, 5, (300, 32)).astype(np.float32)
+    _, C = run(A, B, 4, 2)
+    assert np.array_equal(C, (dense @ B.astype(np.float64)).astype(np.float32))
+
+
+def test_rows_plan_accumulate_and_spmv():
+    A, B = synth_case(512, 512, 0.20, 4, seed=0x5EED0000 + 9200)
+    C0 = sc_amd.synth_dense(512 * 4, 9201).reshape(512, 4)
+    _, C = run(A, B, 4, 2, accumulate=C0)
+    err, _ = oracle_check(A, B, C - C0)
+    assert err <= 1e-4, err
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 2), sc_amd.PLAN_ROWS)
+    y = plan.spmv(torch.from_numpy(np.ascontiguousarray(B[:, 0])).to(DEV))
+    torch.cuda.synchronize()
+    err, _ = oracle_check(A, B[:, :1], y.cpu().numpy().reshape(-1, 1))
+    assert err <= REL_TOL, err
+
+
+def test_rows_plan_of_km1_file_is_the_plain_plan():
+    A, B = synth_case(128, 128, 0.2, 32, seed=0x5EED0000 + 9300)
+    plan, C = run(A, B, 1, 1)
+    err, _ = oracle_check(A, B, C)
+    assert err <= REL_TOL, err
+    assert "rows of" not in plan.describe(32)
+
+
+@pytest.mark.parametrize("n", [1, 4, 128])
+def test_default_plan_runs_rows_while_gathers_are_small(n):
+    # 512 x 512 at 80 % sparsity: 4 * 52429 * n bytes of B-row gathers in the
+    # one-row layout, far under 128 MiB -> one-row layout, still exact
+    A, B = synth_case(512, 512, 0.20, n, seed=0x5EED0000 + 9400 + n)
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 2))
+    assert plan.describe(n).endswith("(rows of km=4)")
+    assert plan.info()["km"] == 4  # the plan still reports the file's layout
+    Ct = plan.spmm(torch.from_numpy(B).to(DEV))
+    torch.cuda.synchronize()
+    err, _ = oracle_check(A, B, Ct.cpu().numpy())
+    assert err <= REL_TOL, err
+
+
+def test_default_plan_keeps_patterns_for_large_gathers():
+    # 4096 x 4096 structured at 90 % sparsity, N = 128: 4 * 1.68 M * 128 bytes
+    # of one-row gathers (859 MB) -> the km = 4 pattern layout; N = 1 -> rows
+    A = sc_amd.Csr.synth_blocks(4096, 4096, 0.10, 0.05, 0x5EED0000 + 4128)
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1))
+    assert plan.describe(128).startswith("panel_kernel km=4")
+    assert plan.describe(1).endswith("(rows of km=4)")
+    for flags in (sc_amd.PLAN_PATTERNS, sc_amd.PLAN_TILED):
+        assert "rows of" not in sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1), flags).describe(1)
+
+
+def test_rows_and_patterns_flags_are_exclusive():
+    A, _ = synth_case(64, 64, 0.2, 1, seed=0x5EED0000 + 9500)
+    with pytest.raises(sc_amd.LibscError, match="exclusive"):
+        sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1), sc_amd.PLAN_ROWS | sc_amd.PLAN_PATTERNS)
