@@ -431,6 +431,18 @@ def test_c_abi_exports_every_declared_symbol():
     assert declared <= set(sc_amd.EXPORTS)
 
 
+def test_python_plan_flags_match_the_header():
+    import re
+    text = open(os.path.join(os.path.dirname(HERE), "include", "sc_api.h")).read()
+    defs = {m.group(1): int(m.group(2)) for m in re.finditer(r"#define SC_(PLAN_\w+|ACCUMULATE) (\d+)", text)}
+    assert {"PLAN_DROP_PADDING", "PLAN_TILED", "PLAN_CHUNKED", "PLAN_F16_VALUES", "PLAN_ROWS",
+            "PLAN_PATTERNS", "ACCUMULATE"} <= set(defs)
+    for name, value in defs.items():
+        assert getattr(sc_amd, name) == value, name
+    plan_bits = [v for k, v in defs.items() if k.startswith("PLAN_")]
+    assert len(set(plan_bits)) == len(plan_bits) and all(v & (v - 1) == 0 for v in plan_bits)
+
+
 def test_vendor_library_exports_every_declared_symbol():
     from sc_amd import vendor
     declared = _declared(os.path.join(os.path.dirname(HERE), "include", "sc_vendor.h"))

@@ -135,3 +135,41 @@ def test_rows_and_patterns_flags_are_exclusive():
     A, _ = synth_case(64, 64, 0.2, 1, seed=0x5EED0000 + 9500)
     with pytest.raises(sc_amd.LibscError, match="exclusive"):
         sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1), sc_amd.PLAN_ROWS | sc_amd.PLAN_PATTERNS)
+
+
+@pytest.mark.parametrize("n", [3, 5, 33, 256, 300])
+def test_rows_plan_odd_and_wide_n(n):
+    A, B = synth_case(96, 160, 0.15, n, seed=0x5EED0000 + 9600 + n)
+    _, C = run(A, B, 4, 1)
+    err, _ = oracle_check(A, B, C)
+    assert err <= REL_TOL, (n, err)
+
+
+@pytest.mark.parametrize("n", [1, 4, 32, 128])
+@pytest.mark.parametrize("shape", [(64, 8192, 0.25), (8, 65536, 0.2)])
+def test_rows_plan_long_rows(shape, n):
+    # ~2000 entries a row (staged in LDS as a long panel) and ~13000 a row
+    # (over the 64 KiB staging limit: the unstaged path)
+    m, k, d = shape
+    A, B = synth_case(m, k, d, n, seed=0x5EED0000 + 9700 + m + n)
+    _, C = run(A, B, 4, 2)
+    err, _ = oracle_check(A, B, C)
+    assert err <= REL_TOL, (shape, n, err)
+
+
+@pytest.mark.parametrize("waves", [1, 2, 5, 16])
+def test_rows_plan_waves_per_row(waves):
+    A, B = synth_case(128, 2048, 0.3, 64, seed=0x5EED0000 + 9800 + waves)
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1), sc_amd.PLAN_ROWS)
+    Ct = plan.spmm(torch.from_numpy(B).to(DEV), waves=waves)
+    torch.cuda.synchronize()
+    err, _ = oracle_check(A, B, Ct.cpu().numpy())
+    assert err <= REL_TOL, (waves, err)
+
+
+def test_default_plan_of_empty_matrix_overwrites_c():
+    A = sc_amd.Csr.from_arrays(10, 12, np.zeros(11, np.int32), [], [])
+    B = sc_amd.synth_dense(12 * 4, 3).reshape(12, 4)
+    for flags in (0, sc_amd.PLAN_ROWS):
+        _, C = run(A, B, 4, 1, flags)
+        assert np.all(C == 0)
