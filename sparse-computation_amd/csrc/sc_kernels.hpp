@@ -438,6 +438,10 @@ __global__ void __launch_bounds__(1024)
     cs = lc - p0;  // indexed with global slot numbers
     vs = lv - q0;
   };
+  // The panel's first 64 segment descriptors (all of them, nearly always)
+  // load together with the stream rather than after the stage barrier, and
+  // serve every N chunk.
+  const SegLanes first = load_seg_lanes(seg, sg0, min(64, sg1 - sg0));
   if constexpr (STAGE) stage();
   for (int cbase = 0; cbase < N; cbase += LV) {
     const int c0 = cbase + g * V;
@@ -463,7 +467,7 @@ __global__ void __launch_bounds__(1024)
       for (int e = 0; e < V; ++e) acc[r][e] = 0.f;
     for (int g = sg0; g < sg1; g += 64) {
       const int n = min(64, sg1 - g);
-      D::template run_segs<KM, V>(load_seg_lanes(seg, g, n), n, a0, a1, acc, args);
+      D::template run_segs<KM, V>(g == sg0 ? first : load_seg_lanes(seg, g, n), n, a0, a1, acc, args);
     }
     reduce_slot_lanes<KM, V>(acc, L);
     if (W == 1) {
