@@ -173,3 +173,34 @@ def test_default_plan_of_empty_matrix_overwrites_c():
     for flags in (0, sc_amd.PLAN_ROWS):
         _, C = run(A, B, 4, 1, flags)
         assert np.all(C == 0)
+
+
+def test_rows_layout_of_dictionary_file_keeps_the_stored_subset():
+    # A dictionary-mode file (format_generator.py --pattern_dictionary) stores
+    # only the slots whose pattern is in the dictionary; every layout must
+    # compute the product of exactly the entries the file stores.
+    import os
+    here = os.path.dirname(os.path.abspath(__file__))
+    dic = os.path.join(here, "golden", "cfmtx", "dict4_sub.txt")
+    m = k = 256
+    A, B = synth_case(m, k, 0.2, 32, seed=0x5EED0000 + 9900)
+    cf = sc_amd.Cfmtx.build(A, 4, 1, dictionary=dic)
+    # the stored entries, decoded from the file's pattern blocks (the oracle's
+    # decoding rule: slot j of panel q holds row q*4 + r of each '1' at r)
+    kept = np.zeros((m, k))
+    for p in cf.patterns():
+        rows = [r for r, ch in enumerate(p["bits"]) if ch == "1"]
+        for q in range(len(p["rpp"]) - 1):
+            for j in range(p["rpp"][q], p["rpp"][q + 1]):
+                for t, r in enumerate(rows):
+                    if q * 4 + r < m:
+                        kept[q * 4 + r, p["cb"][j]] += p["vals"][j * len(rows) + t]
+    assert 0 < np.count_nonzero(kept) < A.nnz  # the dictionary dropped entries
+    ref = kept @ B.astype(np.float64)
+    bound = np.abs(kept) @ np.abs(B.astype(np.float64))
+    Bt = torch.from_numpy(B).to(DEV)
+    for flags in (0, sc_amd.PLAN_ROWS, sc_amd.PLAN_PATTERNS):
+        C = sc_amd.Plan(cf, flags).spmm(Bt)
+        torch.cuda.synchronize()
+        err = np.max(np.abs(C.cpu().numpy() - ref) / np.maximum(bound, 1e-30))
+        assert err <= REL_TOL, (flags, err)
