@@ -126,8 +126,9 @@ void sc_cfmtx_free(sc_cfmtx *cf);
 /* Without SC_PLAN_ROWS, SC_PLAN_PATTERNS, SC_PLAN_TILED or SC_PLAN_CHUNKED a
  * plan of a kernel_m > 1 file holds both layouts, and sc_spmm / sc_spmv run
  * the one-row layout while its B-row gathers (4 * stored entries * N bytes)
- * total under 128 MiB, the km-row pattern layout above.  sc_spmm_generated
- * and sc_spmm_f16 always run the pattern layout. */
+ * total under 128 MiB, the km-row pattern layout above; sc_spmm_f16 follows
+ * the same rule when the rows fit its LDS staging.  sc_spmm_generated always
+ * runs the pattern layout. */
 
 /* allocateAndCopyMixedFormat (example_cuda/spmm_demo_gpu_utils.h:207-245) and
  * the constructors of the generated classes SpMMMixePatternGeneralCacheLess /

@@ -243,7 +243,8 @@ sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   const std::vector<PatInfo> info = validate(cf);
   std::unique_ptr<sc_plan, void (*)(sc_plan *)> plan(build_plan(cf, flags, info), sc_plan_destroy);
   if (cf.km > 1 && !(flags & (SC_PLAN_PATTERNS | SC_PLAN_TILED | SC_PLAN_CHUNKED))) {
-    plan->rows = create_plan(rows_of(cf, info, (flags & SC_PLAN_DROP_PADDING) != 0), flags & SC_PLAN_DROP_PADDING);
+    plan->rows = create_plan(rows_of(cf, info, (flags & SC_PLAN_DROP_PADDING) != 0),
+                             flags & (SC_PLAN_DROP_PADDING | SC_PLAN_F16_VALUES));
     plan->rows->rows_of_km = cf.km;
   }
   return plan.release();
@@ -779,6 +780,13 @@ int sc_spmm_f16(const sc_plan *plan, const void *dB, void *dC, int32_t N, int32_
     int dev = -1;
     hip_check(hipGetDevice(&dev), "hipGetDevice");
     if (dev != plan->device) throw sc::Error{SC_ERR_ARG, "plan lives on another device than the current one"};
+    // the one-row layout under the same rule as sc_spmm, when its rows fit
+    // the binary16 path's LDS staging
+    const sc_plan *r = layout_for(plan, N);
+    if (r != plan) {
+      const int wr = waves_per_panel ? waves_per_panel : auto_waves(r, N);
+      if (r->view.vals16 && sc::gather_lds(N, wr, r->km, r->view.max_pslots, r->view.max_pvals)) plan = r;
+    }
     int w = waves_per_panel ? waves_per_panel : auto_waves(plan, N);
     if (!sc::gather_lds(N, w, plan->km, plan->view.max_pslots, plan->view.max_pvals))
       throw sc::Error{SC_ERR_UNSUPPORTED, "a panel of this plan does not fit the binary16 path's LDS staging"};

@@ -40,12 +40,18 @@ def within_f16_bound(C16, c, cab):
     return bool(np.all(err <= bound)), float(np.max(err - bound))
 
 
+# 0: the default plan (its one-row layout at these sizes); PLAN_PATTERNS: the
+# km-row pattern layout alone
+LAYOUTS = [0, sc_amd.PLAN_PATTERNS]
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
 @pytest.mark.parametrize("n", [1, 2, 4])
 @pytest.mark.parametrize("km,kn", [(1, 1), (2, 3), (4, 1), (4, 2), (6, 8)])
-def test_spmm_f16_matches_rounded_product(km, kn, n):
+def test_spmm_f16_matches_rounded_product(km, kn, n, layout):
     A, B = synth_case(515, 700, 0.15, n, seed=0x5EED0000 + 9950 + km * 10 + kn + n, sigma=0.5)
     B16 = B.astype(np.float16)
-    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, km, kn), sc_amd.PLAN_F16_VALUES)
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, km, kn), sc_amd.PLAN_F16_VALUES | layout)
     C16 = plan.spmm_f16(torch.from_numpy(B16).to(DEV)).cpu().numpy()
     c, cab = f16_reference(A, B16)
     ok, worst = within_f16_bound(C16, c, cab)
@@ -55,12 +61,13 @@ def test_spmm_f16_matches_rounded_product(km, kn, n):
     assert C32.dtype == np.float32 and np.isfinite(C32).all()
 
 
+@pytest.mark.parametrize("layout", LAYOUTS)
 @pytest.mark.parametrize("waves", [1, 8])
-def test_spmm_f16_accumulate(waves):
+def test_spmm_f16_accumulate(waves, layout):
     A, B = synth_case(256, 300, 0.2, 4, seed=0x5EED0000 + 9990 + waves, sigma=0.5)
     B16 = B.astype(np.float16)
     C0 = sc_amd.synth_dense(256 * 4, 23).reshape(256, 4).astype(np.float16)
-    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1), sc_amd.PLAN_F16_VALUES)
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1), sc_amd.PLAN_F16_VALUES | layout)
     Ct = torch.from_numpy(C0.copy()).to(DEV)
     plan.spmm_f16(torch.from_numpy(B16).to(DEV), Ct, accumulate=True, waves=waves)
     c, cab = f16_reference(A, B16)
