@@ -312,6 +312,13 @@ sc_plan *build_plan(const sc::Cfmtx &cf, int32_t flags, const std::vector<PatInf
   panel_seg[(size_t)npanels] = (int32_t)seg.size();
   panel_slot[(size_t)npanels] = (int32_t)cols.size();
   panel_val[(size_t)npanels] = (int32_t)vals.size();
+  // km = 1: the slots of each row's segment, for the N = 1 row kernel
+  std::vector<int32_t> row_len;
+  if (km == 1) {
+    row_len.assign((size_t)npanels, 0);
+    for (int32_t q = 0; q < npanels; ++q)
+      for (int32_t si = panel_seg[(size_t)q]; si < panel_seg[(size_t)q + 1]; ++si) row_len[(size_t)q] += seg[(size_t)si].z;
+  }
 
   // K-block-major copy of the stream: for K block kb and panel p, the part
   // of each of p's segments whose columns fall in the block, contiguous per
@@ -511,7 +518,8 @@ sc_plan *build_plan(const sc::Cfmtx &cf, int32_t flags, const std::vector<PatInf
   size_t off_timg = align_up<int>(off_tvals + tvals.size() * sizeof(float));
   size_t off_toff = align_up<int>(off_timg + timg.size() * sizeof(int32_t));
   size_t off_v16 = align_up<int>(off_toff + toff.size() * sizeof(int32_t));
-  size_t total = align_up<int>(off_v16 + vals16.size() * sizeof(_Float16));
+  size_t off_rowlen = align_up<int>(off_v16 + vals16.size() * sizeof(_Float16));
+  size_t total = align_up<int>(off_rowlen + row_len.size() * sizeof(int32_t));
   hip_check(hipMalloc(&plan->dmem, total), "hipMalloc(plan)");
   std::vector<unsigned char> host(total, 0);
   std::memcpy(host.data() + off_seg, seg.data(), seg.size() * sizeof(int4));
@@ -529,6 +537,7 @@ sc_plan *build_plan(const sc::Cfmtx &cf, int32_t flags, const std::vector<PatInf
   std::memcpy(host.data() + off_v16, vals16.data(), vals16.size() * sizeof(_Float16));
   std::memcpy(host.data() + off_timg, timg.data(), timg.size() * sizeof(int32_t));
   std::memcpy(host.data() + off_toff, toff.data(), toff.size() * sizeof(int32_t));
+  std::memcpy(host.data() + off_rowlen, row_len.data(), row_len.size() * sizeof(int32_t));
   hipError_t e = hipMemcpy(plan->dmem, host.data(), total, hipMemcpyHostToDevice);
   if (e != hipSuccess) {
     (void)hipFree(plan->dmem);
@@ -571,6 +580,7 @@ sc_plan *build_plan(const sc::Cfmtx &cf, int32_t flags, const std::vector<PatInf
   plan->view.kblock_kind = kind;
   plan->view.a_bytes = 4ll * ((long long)cols.size() + (long long)vals.size());
   plan->view.vals16 = vals16.empty() ? nullptr : (const _Float16 *)(base + off_v16);
+  plan->view.row_len = row_len.empty() ? nullptr : (const int *)(base + off_rowlen);
   return plan.release();
 }
 
@@ -722,7 +732,10 @@ int sc_plan_describe(const sc_plan *p, int32_t N, char *buf, size_t buflen) {
       const int w = auto_waves(p, N);
       const sc::Geometry g = sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes,
                                    p->nslots / std::max(1, p->npanels));
-      if (!g.wide && sc::gather_lds_f32(N, w, p->km, p->view.max_pslots, p->view.max_pvals)) {
+      if (sc::use_row_spmv(p->view, p->km, N, w)) {
+        d = "row_spmv_kernel km=1 rows_per_workgroup=" + std::to_string(sc::kRowSpmvRows) + " grid=" +
+            std::to_string((p->M + sc::kRowSpmvRows - 1) / sc::kRowSpmvRows);
+      } else if (!g.wide && sc::gather_lds_f32(N, w, p->km, p->view.max_pslots, p->view.max_pvals)) {
         d = "gather_kernel km=" + std::to_string(p->km) + " V=" + std::to_string(N) + " waves=" +
             std::to_string(w) + " grid=" + std::to_string(p->npanels);
       } else {
