@@ -1510,7 +1510,9 @@ inline Geometry geometry(int km, int N, int W, long long K = 0, int max_pslots =
 // shortest dependent chain a row has: its offsets, its stream, x, the store.
 // Measured on MI355X against the lanes-over-slots kernel (graph replay): SpMV
 // 512^2 at 70 % sparsity 2.92 -> 2.23 us, small-B 512^2 N = 1 (rows of km 4)
-// 2.79 -> 2.16, structured 4096^2 N = 1 7.63 -> 7.03.
+// 2.79 -> 2.16, structured 4096^2 N = 1 7.63 -> 7.03; non-temporal stream
+// loads then took the structured case from 6.99 to 6.20 us (2.20 -> 2.07 on
+// the 512^2 SpMV).
 constexpr int kRowSpmvRows = 4;  // rows (waves) per workgroup
 template <int ROWS>
 __global__ void __launch_bounds__(64 * ROWS)
@@ -1527,8 +1529,10 @@ __global__ void __launch_bounds__(64 * ROWS)
   const int nq = (n + 3) >> 2;
   float acc = 0.f;
   for (int q = lane; q < nq; q += 64) {
-    const vec4i c = c4[q];
-    const vec4f v = v4[q];
+    // the stream is read once: non-temporal loads keep it from displacing x
+    // and the neighbouring rows' lines in the caches
+    const vec4i c = __builtin_nontemporal_load(c4 + q);
+    const vec4f v = __builtin_nontemporal_load(v4 + q);
     const int e = q * 4;
     const float x0 = x[c.x];  // e < n for every q < nq
     const float x1 = e + 1 < n ? x[c.y] : 0.f;
