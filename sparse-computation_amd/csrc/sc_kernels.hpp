@@ -1502,23 +1502,34 @@ inline Geometry geometry(int km, int N, int W, long long K = 0, int max_pslots =
   return g;
 }
 
-// SpMV (N = 1) on one-row panels (km = 1): one wave per row, four rows per
-// workgroup.  A lane reads four consecutive slots' columns and values with one
-// 16-byte load each (every panel starts on a 16-byte boundary), gathers their
-// four x values and accumulates; the row's tail past its last slot is masked,
-// never read from x; the wave reduces with a butterfly of shuffles.  The
-// shortest dependent chain a row has: its offsets, its stream, x, the store.
+// SpMV / narrow SpMM (N = 1, 2, 4) on one-row panels (km = 1): one wave per
+// row, four rows per workgroup.  A lane reads four consecutive slots' columns
+// and values with one 16-byte load each (every panel starts on a 16-byte
+// boundary), gathers their four B rows (N floats each, one 4-, 8- or 16-byte
+// load) and accumulates; slots past the row's last one are masked, never read
+// from B; the wave reduces with a butterfly of shuffles.  The shortest
+// dependent chain a row has: its offsets, its stream, B, the store.
 // Measured on MI355X against the lanes-over-slots kernel (graph replay): SpMV
 // 512^2 at 70 % sparsity 2.92 -> 2.23 us, small-B 512^2 N = 1 (rows of km 4)
 // 2.79 -> 2.16, structured 4096^2 N = 1 7.63 -> 7.03; non-temporal stream
 // loads then took the structured case from 6.99 to 6.20 us (2.20 -> 2.07 on
 // the 512^2 SpMV).
 constexpr int kRowSpmvRows = 4;  // rows (waves) per workgroup
-template <int ROWS>
+template <int V>
+__device__ __forceinline__ vec4f row_of(const float *__restrict__ B, int col) {
+  if constexpr (V == 4) return *reinterpret_cast<const vec4f *>(B + (size_t)col * 4);
+  else if constexpr (V == 2) {
+    const vec2f t = *reinterpret_cast<const vec2f *>(B + (size_t)col * 2);
+    return vec4f{t.x, t.y, 0.f, 0.f};
+  } else {
+    return vec4f{B[col], 0.f, 0.f, 0.f};
+  }
+}
+template <int ROWS, int V>
 __global__ void __launch_bounds__(64 * ROWS)
     row_spmv_kernel(const int *__restrict__ panel_slot, const int *__restrict__ panel_val,
                     const int *__restrict__ row_len, const int *__restrict__ cols,
-                    const float *__restrict__ vals, const float *__restrict__ x, float *__restrict__ y, int M,
+                    const float *__restrict__ vals, const float *__restrict__ B, float *__restrict__ C, int M,
                     int accumulate) {
   const int row = blockIdx.x * ROWS + (int)(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -1527,30 +1538,65 @@ __global__ void __launch_bounds__(64 * ROWS)
   const vec4f *v4 = reinterpret_cast<const vec4f *>(vals + panel_val[row]);
   const int n = row_len[row];
   const int nq = (n + 3) >> 2;
-  float acc = 0.f;
+  float acc[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) acc[k] = 0.f;
+  // the stream is read once: non-temporal loads keep it from displacing B
+  // and the neighbouring rows' lines in the caches
+  if constexpr (V == 1) {
+    // scalar B values
+    for (int q = lane; q < nq; q += 64) {
+      const vec4i c = __builtin_nontemporal_load(c4 + q);
+      const vec4f v = __builtin_nontemporal_load(v4 + q);
+      const int e = q * 4;
+      const float x0 = B[c.x];  // e < n for every q < nq
+      const float x1 = e + 1 < n ? B[c.y] : 0.f;
+      const float x2 = e + 2 < n ? B[c.z] : 0.f;
+      const float x3 = e + 3 < n ? B[c.w] : 0.f;
+      acc[0] = __builtin_fmaf(v.x, x0, acc[0]);
+      if (e + 1 < n) acc[0] = __builtin_fmaf(v.y, x1, acc[0]);
+      if (e + 2 < n) acc[0] = __builtin_fmaf(v.z, x2, acc[0]);
+      if (e + 3 < n) acc[0] = __builtin_fmaf(v.w, x3, acc[0]);
+    }
+  } else
   for (int q = lane; q < nq; q += 64) {
-    // the stream is read once: non-temporal loads keep it from displacing x
-    // and the neighbouring rows' lines in the caches
     const vec4i c = __builtin_nontemporal_load(c4 + q);
     const vec4f v = __builtin_nontemporal_load(v4 + q);
     const int e = q * 4;
-    const float x0 = x[c.x];  // e < n for every q < nq
-    const float x1 = e + 1 < n ? x[c.y] : 0.f;
-    const float x2 = e + 2 < n ? x[c.z] : 0.f;
-    const float x3 = e + 3 < n ? x[c.w] : 0.f;
-    acc = __builtin_fmaf(v.x, x0, acc);
-    if (e + 1 < n) acc = __builtin_fmaf(v.y, x1, acc);
-    if (e + 2 < n) acc = __builtin_fmaf(v.z, x2, acc);
-    if (e + 3 < n) acc = __builtin_fmaf(v.w, x3, acc);
+    const vec4f zero = {0.f, 0.f, 0.f, 0.f};
+    const vec4f b0 = row_of<V>(B, c.x);  // e < n for every q < nq
+    const vec4f b1 = e + 1 < n ? row_of<V>(B, c.y) : zero;
+    const vec4f b2 = e + 2 < n ? row_of<V>(B, c.z) : zero;
+    const vec4f b3 = e + 3 < n ? row_of<V>(B, c.w) : zero;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      acc[k] = __builtin_fmaf(v.x, b0[k], acc[k]);
+      if (e + 1 < n) acc[k] = __builtin_fmaf(v.y, b1[k], acc[k]);
+      if (e + 2 < n) acc[k] = __builtin_fmaf(v.z, b2[k], acc[k]);
+      if (e + 3 < n) acc[k] = __builtin_fmaf(v.w, b3[k], acc[k]);
+    }
   }
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
-  if (lane == 0) y[row] = accumulate ? y[row] + acc : acc;
+  for (int k = 0; k < V; ++k)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc[k] += __shfl_xor(acc[k], o);
+  if (lane == 0) {
+    float *dst = C + (size_t)row * V;
+    // a branch, not a select: C is read only when accumulating (a select
+    // made the compiler load C on every launch, +0.3 us at 512^2)
+    if (accumulate) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) dst[k] += acc[k];
+    } else {
+#pragma unroll
+      for (int k = 0; k < V; ++k) dst[k] = acc[k];
+    }
+  }
 }
 
-// The launch row_spmv_kernel takes: km = 1, N = 1, one wave per row.
+// The launches row_spmv_kernel takes: km = 1, N = 1, 2 or 4, one wave per row.
 inline bool use_row_spmv(const DevView &v, int km, int N, int W) {
-  return km == 1 && N == 1 && W == 1 && v.row_len != nullptr;
+  return km == 1 && (N == 1 || N == 2 || N == 4) && W == 1 && v.row_len != nullptr;
 }
 
 template <int KM, class D>
@@ -1558,9 +1604,14 @@ hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int 
                          int pack, hipStream_t stream) {
   if (v.npanels <= 0 || N <= 0) return hipSuccess;
   if (use_row_spmv(v, KM, N, W)) {
-    hipLaunchKernelGGL(row_spmv_kernel<kRowSpmvRows>, dim3((unsigned)((v.M + kRowSpmvRows - 1) / kRowSpmvRows)),
-                       dim3(64u * kRowSpmvRows), 0, stream, v.panel_slot, v.panel_val, v.row_len, v.cols,
-                       v.vals, B, C, v.M, accumulate);
+    const dim3 rgrid((unsigned)((v.M + kRowSpmvRows - 1) / kRowSpmvRows)), rblock(64u * kRowSpmvRows);
+#define SC_ROW(VV)                                                                                       \
+  hipLaunchKernelGGL((row_spmv_kernel<kRowSpmvRows, VV>), rgrid, rblock, 0, stream, v.panel_slot,      \
+                     v.panel_val, v.row_len, v.cols, v.vals, B, C, v.M, accumulate)
+    if (N == 4) SC_ROW(4);
+    else if (N == 2) SC_ROW(2);
+    else SC_ROW(1);
+#undef SC_ROW
     return hipGetLastError();
   }
   const TileGeometry tg = tile_geometry(v, N);

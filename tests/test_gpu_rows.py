@@ -206,31 +206,32 @@ def test_rows_layout_of_dictionary_file_keeps_the_stored_subset():
         assert err <= REL_TOL, (flags, err)
 
 
+@pytest.mark.parametrize("n", [1, 2, 4])
 @pytest.mark.parametrize("kn,drop", [(1, 0), (3, 0), (3, sc_amd.PLAN_DROP_PADDING)])
 @pytest.mark.parametrize("accumulate", [False, True])
-def test_row_spmv_kernel_tails_empty_rows_padding(kn, drop, accumulate):
-    # N = 1 on one-row panels runs row_spmv_kernel: rows of every length mod 4
-    # (0..9 entries and longer), empty rows, kn padding kept or dropped
+def test_row_spmv_kernel_tails_empty_rows_padding(kn, drop, accumulate, n):
+    # N = 1, 2, 4 on one-row panels runs row_spmv_kernel: rows of every length
+    # mod 4 (0..9 entries and longer), empty rows, kn padding kept or dropped
     rng = np.random.default_rng(13 + kn)
     m, k = 203, 300
     lens = np.concatenate([np.arange(10), rng.integers(0, 120, m - 10)])
     dense = np.zeros((m, k))
-    for i, n in enumerate(lens):
-        dense[i, rng.choice(k, size=int(n), replace=False)] = rng.standard_normal(int(n))
+    for i, ln in enumerate(lens):
+        dense[i, rng.choice(k, size=int(ln), replace=False)] = rng.standard_normal(int(ln))
     ip = np.concatenate([[0], np.cumsum((dense != 0).sum(1))]).astype(np.int32)
     ix = np.nonzero(dense)[1].astype(np.int32)
     dx = dense[dense != 0].astype(np.float32).astype(np.float64)
     A = sc_amd.Csr.from_arrays(m, k, ip, ix, dx)
-    B = sc_amd.synth_dense(k, 99).reshape(k, 1)
+    B = sc_amd.synth_dense(k * n, 99).reshape(k, n)
     for km in (1, 4):
         plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, km, kn), sc_amd.PLAN_ROWS | drop)
-        assert plan.describe(1).startswith("row_spmv_kernel")
-        C0 = sc_amd.synth_dense(m, 100).reshape(m, 1)
-        Ct = torch.from_numpy(C0.copy() if accumulate else np.full((m, 1), np.nan, np.float32)).to(DEV)
+        assert plan.describe(n).startswith(f"row_spmv_kernel km=1 V={n}")
+        C0 = sc_amd.synth_dense(m * n, 100).reshape(m, n)
+        Ct = torch.from_numpy(C0.copy() if accumulate else np.full((m, n), np.nan, np.float32)).to(DEV)
         plan.spmm(torch.from_numpy(B).to(DEV), Ct, accumulate=accumulate)
         torch.cuda.synchronize()
         C = Ct.cpu().numpy() - (C0 if accumulate else 0)
         err, _ = oracle_check(A, B, C)
-        assert err <= (1e-4 if accumulate else REL_TOL), (km, kn, drop, err)
+        assert err <= (1e-4 if accumulate else REL_TOL), (km, kn, drop, n, err)
         if not accumulate:
             assert np.all(C[lens == 0] == 0)
