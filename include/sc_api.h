@@ -87,12 +87,12 @@ int sc_cfmtx_build(const sc_csr *A, int32_t km, int32_t kn, const char *dictiona
                    sc_cfmtx **out);
 /* format_writer (format_generator.py:132-160), byte-exact. */
 int sc_cfmtx_write(const sc_cfmtx *cf, const char *path);
-/* readCFMTXFile / readCompressedFormatMatrix (utils/Sparse_io.cpp:84-182, :243-250). */
+/* readCFMTXFile / readCompressedFormatMatrix (utils/Sparse_io.cpp:84-182, :208-215). */
 int sc_cfmtx_read(const char *path, sc_cfmtx **out);
-/* loadCfmtxMatrices (utils/Sparse_io.cpp:221-231, include/Sparse_io.h:17-24):
+/* loadCfmtxMatrices (utils/Sparse_io.cpp:186-196, include/Sparse_io.h:24):
  * the .cfmtx and its companion .mtx (sym_lib reader).  Path must end in .cfmtx. */
 int sc_load_cfmtx_matrices(const char *cfmtx_path, sc_csr **csr, sc_cfmtx **cf);
-/* readCSRMatrix (utils/Sparse_io.cpp:233-241): the companion .mtx only. */
+/* readCSRMatrix (utils/Sparse_io.cpp:198-206): the companion .mtx only. */
 int sc_read_csr_matrix(const char *cfmtx_path, sc_csr **csr);
 /* companionMtxPathFromCFMTX (utils/Sparse_io.cpp:28-46). */
 int sc_companion_mtx_path(const char *cfmtx_path, char *buf, size_t buflen);
@@ -162,7 +162,7 @@ int sc_spmv(const sc_plan *plan, const float *dx, float *dy, int32_t flags, void
  * IEEE binary16, N = 1, 2 or 4, fp32 accumulation, C rounded once to nearest
  * even.  Replaces the reference's fp16 small-B kernels
  * (SpmvComplexPatternDecomposeByRowSeperatedHalf, PatternWith{pop}NNZByRowPanelFullHALF:
- * example_cuda/spmm_small_b_col_demo_gpu_utils.h:2987-4910, generator
+ * example_cuda/spmm_small_b_col_demo_gpu_utils.h:2987-5017, generator
  * code_gen/spmm_small_b_col/spmm_small_b_col_format_code_generator.py:326-435),
  * which accumulate in binary16. */
 int sc_spmm_f16(const sc_plan *plan, const void *dB, void *dC, int32_t N, int32_t flags,

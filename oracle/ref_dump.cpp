@@ -4,9 +4,9 @@
 // product's reader, never part of the product.
 //
 //   ref_cfmtx_dump cfmtx <file.cfmtx>  -> readCompressedFormatMatrix
-//                                         (utils/Sparse_io.cpp:243-250)
+//                                         (utils/Sparse_io.cpp:208-215)
 //   ref_cfmtx_dump csr   <file.cfmtx>  -> readCSRMatrix on the companion .mtx
-//                                         (utils/Sparse_io.cpp:233-241)
+//                                         (utils/Sparse_io.cpp:198-206)
 //
 // Output (text): floats as the hex of their bit patterns so nothing is lost.
 #include <cstdint>

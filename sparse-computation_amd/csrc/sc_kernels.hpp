@@ -18,9 +18,9 @@
 //   * per lane the C tile is acc[KM][V] in VGPRs; a pattern body adds
 //     value(slot,row) * B[col(slot), c0 .. c0+V) into the rows of its mask
 //     only, with the row indices compile-time constants;
-//   * the S slot sub-lanes are reduced with a butterfly (ds_swizzle / DPP
-//     through __shfl_xor), then the W waves through LDS in a fixed order, so
-//     results are deterministic run to run.
+//   * the S slot sub-lanes are reduced with a butterfly of cross-lane moves,
+//     then the W waves through LDS in a fixed order, so results are
+//     deterministic run to run.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -1599,6 +1599,21 @@ inline bool use_row_spmv(const DevView &v, int km, int N, int W) {
   return km == 1 && (N == 1 || N == 2 || N == 4) && W == 1 && v.row_len != nullptr;
 }
 
+// The buffer-descriptor form of the lanes-over-slots kernel forms a B-row
+// offset as __umul24(row, N * 4) + lane bytes: every operand of the 24-bit
+// multiply must fit 24 bits (K below 2^24 rows, N * 4 below 2^24 bytes) and
+// the offsets the descriptor's 31-bit range (B below 2 GiB).  Other shapes
+// take the 64-bit pointer form.
+constexpr bool buffer_offsets_fit(long long K, long long N) {
+  return K * N * (long long)sizeof(float) < (1ll << 31) && K < (1ll << 24) && N * (long long)sizeof(float) < (1ll << 24);
+}
+static_assert(buffer_offsets_fit(4096, 128) && buffer_offsets_fit((1 << 24) - 1, 1) &&
+                  buffer_offsets_fit(127, (1 << 22) - 1),
+              "shapes inside the 24-bit multiply take the buffer path");
+static_assert(!buffer_offsets_fit(127, 1 << 22) && !buffer_offsets_fit(1 << 24, 1) &&
+                  !buffer_offsets_fit(1 << 15, 1 << 14),
+              "row bytes of 2^24, 2^24 rows or 2 GiB of B take the pointer path");
+
 template <int KM, class D>
 hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int accumulate, int W,
                          int pack, hipStream_t stream) {
@@ -1672,10 +1687,7 @@ hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int 
   hipLaunchKernelGGL((panel_kernel<KM, VV, ST, D, AA>), grid, block, g.lds, stream, v.seg, v.panel_seg,  \
                      v.panel_slot, v.panel_val, v.cols, v.vals, B, C, v.M, v.K, N, g.L, accumulate, pack, \
                      g.stage_cols)
-  // B below 2 GiB: byte offsets stay inside the buffer descriptor's 31-bit
-  // range; K below 2^24: row numbers fit the 24-bit multiply
-  const bool buf = (long long)v.K * N * (long long)sizeof(float) < (1ll << 31) && v.K < (1 << 24);
-  if (buf) {
+  if (buffer_offsets_fit(v.K, N)) {
     if (g.stage) {
       if (g.V == 4) SC_NARROW(4, true, SegArgsBuf);
       else if (g.V == 2) SC_NARROW(2, true, SegArgsBuf);

@@ -54,6 +54,8 @@ class Plan:
         check(lib().sc_plan_create(cf._h, flags, C.byref(h)))
         self._h = h
         self._free = lib().sc_plan_destroy
+        # sc_plan_create uploads to the current HIP device
+        self.device = torch.cuda.current_device()
 
     def __del__(self):
         # the free function is bound at creation: at interpreter exit this
@@ -76,10 +78,15 @@ class Plan:
         check(lib().sc_plan_describe(self._h, N, buf, len(buf)))
         return buf.value.decode()
 
-    @staticmethod
-    def _check_operand(t, rows, cols, name):
-        if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()):
-            raise ValueError(f"{name} must be a contiguous float32 tensor on the GPU")
+    def _check_device(self, t, name):
+        if not t.is_cuda or t.device.index != self.device:
+            raise ValueError(f"{name} must be on the plan's device cuda:{self.device}, got {t.device}")
+
+    def _check_operand(self, t, rows, cols, name, dtype=None):
+        dtype = torch.float32 if dtype is None else dtype
+        if not (t.is_cuda and t.dtype == dtype and t.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous {dtype} tensor on the GPU")
+        self._check_device(t, name)
         if t.numel() != rows * cols:
             raise ValueError(f"{name} must hold {rows}x{cols} elements, got {tuple(t.shape)}")
 
@@ -123,11 +130,13 @@ class Plan:
         N = B.shape[1] if B.dim() == 2 else 1
         if B.dtype != torch.float16 or not B.is_cuda or not B.is_contiguous() or B.shape[0] != info["n"]:
             raise ValueError(f"B must be a contiguous ({info['n']}, N) float16 device tensor")
+        self._check_device(B, "B")
         if C_out is None:
             C_out = torch.empty((info["m"], N), dtype=torch.float16, device=B.device)
-        if (C_out.dtype != torch.float16 or not C_out.is_contiguous() or C_out.shape[0] != info["m"]
-                or C_out.numel() != info["m"] * N):
+        if (C_out.dtype != torch.float16 or not C_out.is_cuda or not C_out.is_contiguous()
+                or C_out.shape[0] != info["m"] or C_out.numel() != info["m"] * N):
             raise ValueError(f"C must be a contiguous ({info['m']}, {N}) float16 device tensor")
+        self._check_device(C_out, "C")
         check(lib().sc_spmm_f16(self._h, C.c_void_p(B.data_ptr()), C.c_void_p(C_out.data_ptr()), N,
                                 ACCUMULATE if accumulate else 0, waves, _stream_handle(stream)))
         return C_out

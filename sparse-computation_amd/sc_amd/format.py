@@ -160,21 +160,21 @@ class Cfmtx:
 
 
 def load_cfmtx_matrices(path: str):
-    """loadCfmtxMatrices (utils/Sparse_io.cpp:221-231): (Csr, Cfmtx)."""
+    """loadCfmtxMatrices (utils/Sparse_io.cpp:186-196): (Csr, Cfmtx)."""
     a, c = C.c_void_p(), C.c_void_p()
     check(lib().sc_load_cfmtx_matrices(path.encode(), C.byref(a), C.byref(c)))
     return Csr(a), Cfmtx(c)
 
 
 def read_csr_matrix(path: str) -> Csr:
-    """readCSRMatrix (utils/Sparse_io.cpp:233-241)."""
+    """readCSRMatrix (utils/Sparse_io.cpp:198-206)."""
     a = C.c_void_p()
     check(lib().sc_read_csr_matrix(path.encode(), C.byref(a)))
     return Csr(a)
 
 
 def read_compressed_format_matrix(path: str) -> Cfmtx:
-    """readCompressedFormatMatrix (utils/Sparse_io.cpp:243-250)."""
+    """readCompressedFormatMatrix (utils/Sparse_io.cpp:208-215)."""
     if not path.endswith(".cfmtx"):
         raise ValueError(f"readCompressedFormatMatrix expects a .cfmtx path: {path}")
     return Cfmtx.read(path)

@@ -26,6 +26,18 @@ def csr_f32(A):
     return ip, ix, dx.astype(np.float32)
 
 
+def oracle_check_acc(A, B, C_gpu, C0):
+    """Max relative error of an accumulating launch (C = C0 + A*B): C itself
+    against c64 + C0, normalised by (|A| |B|)_ij + |C0_ij|, the forward-error
+    scale of the dot product plus the one extra addition."""
+    m, _ = A.shape
+    n = B.shape[1]
+    ip, ix, ax = csr_f32(A)
+    c64, cab = O.spmm_f64(m, n, ip, ix, ax, B)
+    c0 = np.asarray(C0, np.float64).reshape(m, n)
+    return O.max_rel_err(np.asarray(C_gpu).reshape(m, n), c64 + c0, cab + np.abs(c0))
+
+
 def oracle_check(A, B, C_gpu, tol=REL_TOL):
     """(max_rel_err, max elementwise rel err with floor 1e-6 max|C|)."""
     m, _ = A.shape

@@ -450,3 +450,77 @@ def test_vendor_library_exports_every_declared_symbol():
     lib = vendor.vlib()
     missing = [s for s in sorted(declared) if not hasattr(lib, s)]
     assert not missing, missing
+
+
+class _FakeDeviceTensor:
+    """Stands in for a tensor on cuda:<index> in a process without a GPU: the
+    operand checks of sc_amd.Plan read only these attributes."""
+
+    def __init__(self, shape, dtype, cuda=True, index=0):
+        import torch
+        self.shape = shape
+        self.dtype = dtype
+        self.is_cuda = cuda
+        self.device = torch.device(f"cuda:{index}") if cuda else torch.device("cpu")
+
+    def dim(self):
+        return len(self.shape)
+
+    def numel(self):
+        n = 1
+        for s in self.shape:
+            n *= s
+        return n
+
+    def is_contiguous(self):
+        return True
+
+    def data_ptr(self):  # a launch would need it: the checks must raise first
+        raise AssertionError("operand checks let a launch through")
+
+
+def _bare_plan(m, k):
+    p = object.__new__(sc_amd.Plan)
+    p._h = None
+    p.device = 0
+    p.info = lambda: {"m": m, "n": k}
+    return p
+
+
+def test_plan_rejects_host_or_foreign_operands_before_launch():
+    import torch
+    p = _bare_plan(8, 6)
+    B16 = _FakeDeviceTensor((6, 4), torch.float16)
+    # binary16 path: C on the host, or on another device than the plan's
+    with pytest.raises(ValueError, match="C must"):
+        p.spmm_f16(B16, torch.empty((8, 4), dtype=torch.float16))
+    with pytest.raises(ValueError, match="plan's device"):
+        p.spmm_f16(B16, _FakeDeviceTensor((8, 4), torch.float16, index=1))
+    with pytest.raises(ValueError, match="plan's device"):
+        p.spmm_f16(_FakeDeviceTensor((6, 4), torch.float16, index=1))
+    # fp32 path: the same checks
+    B32 = _FakeDeviceTensor((6, 4), torch.float32)
+    with pytest.raises(ValueError, match="C must"):
+        p.spmm(B32, torch.empty((8, 4), dtype=torch.float32))
+    with pytest.raises(ValueError, match="plan's device"):
+        p.spmm(B32, _FakeDeviceTensor((8, 4), torch.float32, index=1))
+    with pytest.raises(ValueError, match="x must"):
+        p.spmv(torch.empty(6, dtype=torch.float32))
+
+
+def test_committed_reference_matrix_is_the_reference_file(reference_matrix_dir):
+    # the gzipped copies under tests/golden/reference_matrix are the
+    # reference's own fixture files byte for byte
+    from conftest import GOLDEN_FILES
+    if not os.path.isdir(REF_MATRICES):
+        pytest.skip("reference tree not mounted")
+    for name in GOLDEN_FILES:
+        with open(os.path.join(REF_MATRICES, name), "rb") as a, \
+                open(os.path.join(reference_matrix_dir, name), "rb") as b:
+            assert a.read() == b.read(), name
+    # and the unpacked pair loads like the reference's loader does
+    A, cf = sc_amd.load_cfmtx_matrices(os.path.join(reference_matrix_dir, FIXTURE_STEM + "-4-2.cfmtx"))
+    assert A.shape == (512, 512) and A.nnz == 104857
+    built = sc_amd.Cfmtx.build(sc_amd.Csr.from_mtx(os.path.join(reference_matrix_dir, FIXTURE_STEM + ".mtx")), 4, 2)
+    with open(os.path.join(reference_matrix_dir, FIXTURE_STEM + "-4-2.cfmtx")) as f:
+        assert built.text() == f.read()

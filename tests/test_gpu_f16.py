@@ -3,7 +3,7 @@ binary16 B and C, N = 1, 2, 4, fp32 accumulation, C rounded once) against the
 fp64 product of the same binary16 operands.
 
 The reference's fp16 small-B kernels (PatternWith{pop}NNZByRowPanelFullHALF,
-example_cuda/spmm_small_b_col_demo_gpu_utils.h:2987-4910) accumulate in
+example_cuda/spmm_small_b_col_demo_gpu_utils.h:2987-5017) accumulate in
 binary16 and are never run by a reference driver, so there is no reference
 output to match bit for bit; the bar here is the rounding bound of one
 binary16 rounding of an fp32-accumulated sum: |C - exact| <= 2^-11 |exact| +

@@ -15,7 +15,7 @@ import pytest
 import oracle as O
 import sc_amd
 from cases import REL_TOL, csr_f32, oracle_check, synth_case
-from conftest import FIXTURE_STEM, REF_MATRICES
+from conftest import FIXTURE_STEM
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -132,15 +132,11 @@ def test_spmm_structured_4096(n, flags):
 
 
 @pytest.mark.parametrize("km,kn", [(4, 2), (4, 3), (2, 5), (6, 8), (1, 2), (3, 1)])
-def test_fixture_matrix_bit_exact(km, kn):
-    """The reference's own matrix (values 1) times integer B: exact sums."""
-    mtx = os.path.join(REF_MATRICES, FIXTURE_STEM + ".mtx")
-    if os.path.exists(mtx):
-        A = sc_amd.Csr.from_mtx(mtx)
-    else:  # the GPU box has no reference tree: same shape/density, values 1
-        A0 = sc_amd.Csr.synth_uniform(512, 512, 0.4, 1.0, 99)
-        ip, ix, _ = A0.arrays()
-        A = sc_amd.Csr.from_arrays(512, 512, ip, ix, np.ones(len(ix)))
+def test_fixture_matrix_bit_exact(km, kn, reference_matrix_dir):
+    """The reference's own matrix (values 1, committed under tests/golden)
+    times integer B: exact sums."""
+    A = sc_amd.Csr.from_mtx(os.path.join(reference_matrix_dir, FIXTURE_STEM + ".mtx"))
+    assert A.shape == (512, 512) and A.nnz == 104857
     rng = np.random.default_rng(km * 10 + kn)
     for n in (1, 4, 64):
         B = rng.integers(-3, 4, size=(512, n)).astype(np.float32)
@@ -148,6 +144,22 @@ def test_fixture_matrix_bit_exact(km, kn):
         ip, ix, ax = csr_f32(A)
         ref = O.spmm_csr_float(512, n, ip, ix, ax, B)
         assert np.array_equal(C, ref), (km, kn, n)
+
+
+def test_reference_cfmtx_file_bit_exact(reference_matrix_dir):
+    """The reference's own km 4 x kn 2 .cfmtx, read by the .cfmtx reader with
+    its companion .mtx (loadCfmtxMatrices), on every layout: exact sums."""
+    A, cf = sc_amd.load_cfmtx_matrices(os.path.join(reference_matrix_dir, FIXTURE_STEM + "-4-2.cfmtx"))
+    ip, ix, ax = csr_f32(A)
+    rng = np.random.default_rng(42)
+    for n in (1, 4, 32, 128):
+        B = rng.integers(-3, 4, size=(512, n)).astype(np.float32)
+        ref = O.spmm_csr_float(512, n, ip, ix, ax, B)
+        Bt = torch.from_numpy(B).to(DEV)
+        for flags in (0, sc_amd.PLAN_PATTERNS, sc_amd.PLAN_ROWS):
+            C = sc_amd.Plan(cf, flags).spmm(Bt)
+            torch.cuda.synchronize()
+            assert np.array_equal(C.cpu().numpy(), ref), (n, flags)
 
 
 def test_spmv_matches_reference_cpu_path():

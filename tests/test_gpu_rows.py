@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import sc_amd
-from cases import REL_TOL, oracle_check, synth_case
+from cases import REL_TOL, oracle_check, oracle_check_acc, synth_case
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -89,8 +89,8 @@ def test_rows_plan_accumulate_and_spmv():
     A, B = synth_case(512, 512, 0.20, 4, seed=0x5EED0000 + 9200)
     C0 = sc_amd.synth_dense(512 * 4, 9201).reshape(512, 4)
     _, C = run(A, B, 4, 2, accumulate=C0)
-    err, _ = oracle_check(A, B, C - C0)
-    assert err <= 1e-4, err
+    err = oracle_check_acc(A, B, C, C0)
+    assert err <= REL_TOL, err
     plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 2), sc_amd.PLAN_ROWS)
     y = plan.spmv(torch.from_numpy(np.ascontiguousarray(B[:, 0])).to(DEV))
     torch.cuda.synchronize()
@@ -230,8 +230,10 @@ def test_row_spmv_kernel_tails_empty_rows_padding(kn, drop, accumulate, n):
         Ct = torch.from_numpy(C0.copy() if accumulate else np.full((m, n), np.nan, np.float32)).to(DEV)
         plan.spmm(torch.from_numpy(B).to(DEV), Ct, accumulate=accumulate)
         torch.cuda.synchronize()
-        C = Ct.cpu().numpy() - (C0 if accumulate else 0)
-        err, _ = oracle_check(A, B, C)
-        assert err <= (1e-4 if accumulate else REL_TOL), (km, kn, drop, n, err)
+        C = Ct.cpu().numpy()
+        err = oracle_check_acc(A, B, C, C0) if accumulate else oracle_check(A, B, C)[0]
+        assert err <= REL_TOL, (km, kn, drop, n, err)
         if not accumulate:
             assert np.all(C[lens == 0] == 0)
+        else:
+            assert np.array_equal(C[lens == 0], C0[lens == 0])
