@@ -123,6 +123,13 @@ void sc_cfmtx_free(sc_cfmtx *cf);
 #define SC_PLAN_ROWS 16        /* lay the slots out as one-row panels (kernel_m 1):
                                   one workgroup per row instead of per km rows  */
 #define SC_PLAN_PATTERNS 32    /* keep only the km-row pattern layout           */
+#define SC_PLAN_BANDS 64       /* kernel_m 4 files: also build the band layout (B
+                                  staged in LDS once per band of 128 rows and K
+                                  tile, all-ones slots on the matrix cores, split
+                                  K with a plan-owned workspace; the format's
+                                  zero padding slots are skipped); sc_spmm runs it
+                                  at N a multiple of 64 when the layout fits the
+                                  LDS                                            */
 /* Without SC_PLAN_ROWS, SC_PLAN_PATTERNS, SC_PLAN_TILED or SC_PLAN_CHUNKED a
  * plan of a kernel_m > 1 file holds both layouts, and sc_spmm / sc_spmv run
  * the one-row layout while its B-row gathers (4 * stored entries * N bytes)

@@ -15,11 +15,13 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <cstring>
 #include <memory>
 #include <string>
 #include <vector>
 
+#include "sc_band.hpp"
 #include "sc_errors.hpp"
 #include "sc_format.hpp"
 #include "sc_kernels.hpp"
@@ -91,6 +93,14 @@ struct sc_plan {
   mutable long long tcount_n = 0;
   sc::DevView view{};
   GenEntry gen{};
+  // The band layout of a kernel_m 4 plan (SC_PLAN_BANDS): wave images in
+  // band_mem, and the split-K workspace and arrival counters, allocated here
+  // so that no launch allocates (counters zeroed once; every launch leaves
+  // them at zero).
+  sc::BandView band{};
+  void *band_mem = nullptr;
+  float *band_work = nullptr;
+  unsigned *band_cnt = nullptr;
 };
 
 namespace {
@@ -237,11 +247,13 @@ sc_plan *create_rows_plan(const sc::Cfmtx &cf, int32_t flags) {
 }
 
 sc_plan *build_plan(const sc::Cfmtx &cf, int32_t flags, const std::vector<PatInfo> &info);
+void build_band(sc_plan *plan, const sc::Cfmtx &cf, const std::vector<PatInfo> &info);
 
 sc_plan *create_plan(const sc::Cfmtx &cf, int32_t flags) {
   if (flags & SC_PLAN_ROWS) return create_rows_plan(cf, flags);
   const std::vector<PatInfo> info = validate(cf);
   std::unique_ptr<sc_plan, void (*)(sc_plan *)> plan(build_plan(cf, flags, info), sc_plan_destroy);
+  if (flags & SC_PLAN_BANDS) build_band(plan.get(), cf, info);
   if (cf.km > 1 && !(flags & (SC_PLAN_PATTERNS | SC_PLAN_TILED | SC_PLAN_CHUNKED))) {
     plan->rows = create_plan(rows_of(cf, info, (flags & SC_PLAN_DROP_PADDING) != 0),
                              flags & (SC_PLAN_DROP_PADDING | SC_PLAN_F16_VALUES));
@@ -584,6 +596,189 @@ sc_plan *build_plan(const sc::Cfmtx &cf, int32_t flags, const std::vector<PatInf
   return plan.release();
 }
 
+// ---- band layout (SC_PLAN_BANDS, kernel_m 4) -----------------------------
+// A panel's stored entries, split for the band kernel: the slots of the
+// all-ones pattern (four values each), and every other slot's entries by
+// panel row.  Each list in ascending column order.
+struct BandPanel {
+  std::vector<std::pair<int32_t, std::array<float, 4>>> dense;
+  std::vector<std::pair<int32_t, float>> rows[4];
+};
+
+struct BandHost {
+  std::vector<int32_t> img, woff;
+  int nbands = 0, ntiles = 0, KT = 0, wimg_dw = 0;
+};
+
+std::vector<BandPanel> band_panels(const sc::Cfmtx &cf, const std::vector<PatInfo> &info, bool drop_pad) {
+  const int32_t npanels = cf.npanels();
+  std::vector<BandPanel> out((size_t)npanels);
+  for (size_t i = 0; i < cf.patterns.size(); ++i) {
+    const sc::Pattern &p = cf.patterns[i];
+    const int pop = info[i].pop;
+    if (pop == 0) continue;
+    int rows[4], nr = 0;
+    for (int b = 0; b < 4; ++b)
+      if (info[i].mask >> b & 1u) rows[nr++] = b;
+    for (int32_t q = 0; q < npanels; ++q) {
+      const int32_t a = p.rpp[(size_t)q];
+      const int32_t e = drop_pad ? unpadded_end(p, pop, a, p.rpp[(size_t)q + 1]) : p.rpp[(size_t)q + 1];
+      BandPanel &bp = out[(size_t)q];
+      for (int32_t j = a; j < e; ++j) {
+        const float *v = &p.val32[(size_t)j * pop];
+        if (info[i].mask == 0xFu) {
+          bp.dense.push_back({p.cb[(size_t)j], {v[0], v[1], v[2], v[3]}});
+        } else {
+          for (int k = 0; k < nr; ++k) bp.rows[rows[k]].push_back({p.cb[(size_t)j], v[k]});
+        }
+      }
+    }
+  }
+  auto by_col = [](const auto &x, const auto &y) { return x.first < y.first; };
+  for (BandPanel &bp : out) {
+    std::stable_sort(bp.dense.begin(), bp.dense.end(), by_col);
+    for (auto &r : bp.rows) std::stable_sort(r.begin(), r.end(), by_col);
+  }
+  return out;
+}
+
+// The wave images for K tiles of KT rows; false when one image would exceed
+// kBandImgMaxDw dwords.  Image layout: sc_band.hpp (BandView).
+bool band_images(const std::vector<BandPanel> &panels, int32_t K, int KT, BandHost &h) {
+  const int32_t npanels = (int32_t)panels.size();
+  h = BandHost{};
+  h.KT = KT;
+  h.ntiles = (K + KT - 1) / KT;
+  h.nbands = (npanels + sc::kBandPanels - 1) / sc::kBandPanels;
+  const int32_t zero_off = KT * sc::kBandRowBytes;  // byte offset of the zero row
+  // cursors into each panel's lists: tiles are visited in order per panel
+  std::vector<size_t> dcur((size_t)npanels, 0), rcur((size_t)npanels * 4, 0);
+  h.woff.reserve((size_t)h.nbands * h.ntiles * sc::kBandWaves + 1);
+  int max_dw = 0;
+  struct Item {
+    int32_t off[4];
+    float v[16];
+  };
+  const Item zero = {{zero_off, zero_off, zero_off, zero_off}, {0.f}};
+  std::vector<Item> dit, sit;
+  for (int b = 0; b < h.nbands; ++b)
+    for (int t = 0; t < h.ntiles; ++t) {
+      const int32_t klo = t * KT, khi = (int32_t)std::min<int64_t>((int64_t)K, (int64_t)klo + KT);
+      for (int w = 0; w < sc::kBandWaves; ++w) {
+        int32_t hdr[sc::kBandImgHeader] = {0};
+        dit.assign(1, zero);
+        sit.clear();
+        for (int pp = 0; pp < 2; ++pp) {
+          const int32_t q = b * sc::kBandPanels + 2 * w + pp;
+          if (q >= npanels) continue;
+          const BandPanel &bp = panels[(size_t)q];
+          // dense slots of the tile, four per item ([row][slot] values)
+          size_t &dc = dcur[(size_t)q];
+          const size_t d0 = dc;
+          while (dc < bp.dense.size() && bp.dense[dc].first < khi) ++dc;
+          for (size_t j = d0; j < dc; j += 4) {
+            Item it = zero;
+            for (int k = 0; k < 4 && j + k < dc; ++k) {
+              if (bp.dense[j + k].first < klo) throw sc::Error{SC_ERR_INTERNAL, "band layout lost a slot"};
+              it.off[k] = (bp.dense[j + k].first - klo) * sc::kBandRowBytes;
+              for (int i = 0; i < 4; ++i) it.v[4 * i + k] = bp.dense[j + k].second[(size_t)i];
+            }
+            dit.push_back(it);
+          }
+          hdr[pp] = (int32_t)((dc - d0 + 3) / 4);
+          // single entries of the tile, list k = 4 pp + r, four per item; the
+          // list rides in the low bits of the first offset
+          for (int r = 0; r < 4; ++r) {
+            const auto &lst = bp.rows[r];
+            size_t &rc = rcur[(size_t)q * 4 + r];
+            const size_t r0 = rc;
+            while (rc < lst.size() && lst[rc].first < khi) ++rc;
+            for (size_t j = r0; j < rc; j += 4) {
+              Item it = zero;
+              for (int k = 0; k < 4 && j + k < rc; ++k) {
+                if (lst[j + k].first < klo) throw sc::Error{SC_ERR_INTERNAL, "band layout lost an entry"};
+                it.off[k] = (lst[j + k].first - klo) * sc::kBandRowBytes;
+                it.v[k] = lst[j + k].second;
+              }
+              it.off[0] |= 4 * pp + r;
+              sit.push_back(it);
+            }
+          }
+        }
+        while (sit.size() % 4) sit.push_back(zero);
+        const int nd = (int)dit.size(), ns = (int)sit.size();
+        const int dense = sc::kBandImgHeader;
+        const int single = dense + sc::kBandDenseDw * nd;
+        const int total = (single + sc::kBandSingleDw * ns + 3) / 4 * 4;
+        hdr[2] = ns;
+        hdr[3] = dense;
+        hdr[4] = single;
+        hdr[5] = std::max(hdr[0], hdr[1]);
+        if (total > sc::kBandImgMaxDw) return false;
+        max_dw = std::max(max_dw, total);
+        if ((int64_t)h.img.size() + total > INT32_MAX)
+          throw sc::Error{SC_ERR_UNSUPPORTED, "band layout larger than int32 offsets"};
+        h.woff.push_back((int32_t)h.img.size());
+        const size_t o = h.img.size();
+        h.img.resize(o + (size_t)total, 0);
+        std::memcpy(&h.img[o], hdr, sizeof hdr);
+        for (int j = 0; j < nd; ++j) {
+          std::memcpy(&h.img[o + dense + sc::kBandDenseDw * j], dit[j].off, 4 * sizeof(int32_t));
+          std::memcpy(&h.img[o + dense + sc::kBandDenseDw * j + 4], dit[j].v, 16 * sizeof(float));
+        }
+        for (int j = 0; j < ns; ++j) {
+          std::memcpy(&h.img[o + single + sc::kBandSingleDw * j], sit[j].off, 4 * sizeof(int32_t));
+          std::memcpy(&h.img[o + single + sc::kBandSingleDw * j + 4], sit[j].v, 4 * sizeof(float));
+        }
+      }
+    }
+  h.woff.push_back((int32_t)h.img.size());
+  for (int32_t q = 0; q < npanels; ++q) {
+    if (dcur[(size_t)q] != panels[(size_t)q].dense.size()) throw sc::Error{SC_ERR_INTERNAL, "band layout lost slots"};
+    for (int r = 0; r < 4; ++r)
+      if (rcur[(size_t)q * 4 + r] != panels[(size_t)q].rows[r].size())
+        throw sc::Error{SC_ERR_INTERNAL, "band layout lost entries"};
+  }
+  h.wimg_dw = std::max(max_dw, 4);
+  return true;
+}
+
+// Build and upload the band layout of a kernel_m 4 plan: the largest K tile
+// (256 rows down to 32) whose two B stages and sixteen wave images fit the
+// LDS.  A plan whose images fit no tile gets no band layout.
+void build_band(sc_plan *plan, const sc::Cfmtx &cf, const std::vector<PatInfo> &info) {
+  if (cf.km != 4) throw sc::Error{SC_ERR_UNSUPPORTED, "the band layout needs kernel_m 4"};
+  if (cf.n <= 0 || cf.npanels() <= 0) return;
+  // the format's zero padding slots (kernel_n packs) are never computed here:
+  // they repeat their segment's last column with value 0
+  const std::vector<BandPanel> panels = band_panels(cf, info, true);
+  BandHost h;
+  bool ok = false;
+  for (int KT = 256; KT >= 32 && !ok; KT -= 32) {
+    if (!band_images(panels, cf.n, KT, h)) continue;
+    const size_t lds = sc::band_lds_bytes(KT, h.wimg_dw);
+    ok = lds <= sc::kBandLdsBytes;
+  }
+  if (!ok) return;  // the plan runs its other kernels
+  const size_t off_woff = align_up<int>(h.img.size() * sizeof(int32_t));
+  const size_t total = align_up<int>(off_woff + h.woff.size() * sizeof(int32_t));
+  hip_check(hipMalloc(&plan->band_mem, total), "hipMalloc(band layout)");
+  std::vector<unsigned char> host(total, 0);
+  std::memcpy(host.data(), h.img.data(), h.img.size() * sizeof(int32_t));
+  std::memcpy(host.data() + off_woff, h.woff.data(), h.woff.size() * sizeof(int32_t));
+  hip_check(hipMemcpy(plan->band_mem, host.data(), total, hipMemcpyHostToDevice), "hipMemcpy(band layout)");
+  hip_check(hipMalloc((void **)&plan->band_work, sc::kBandWorkFloats * sizeof(float)), "hipMalloc(band workspace)");
+  hip_check(hipMalloc((void **)&plan->band_cnt, sc::kBandCounters * sizeof(unsigned)), "hipMalloc(band counters)");
+  hip_check(hipMemset(plan->band_cnt, 0, sc::kBandCounters * sizeof(unsigned)), "hipMemset(band counters)");
+  hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize(band layout)");
+  plan->band.img = (const int *)plan->band_mem;
+  plan->band.woff = (const int *)((unsigned char *)plan->band_mem + off_woff);
+  plan->band.nbands = h.nbands;
+  plan->band.ntiles = h.ntiles;
+  plan->band.KT = h.KT;
+  plan->band.wimg_dw = h.wimg_dw;
+}
+
 // Waves per panel: enough waves in the grid to cover the 256 CUs several
 // times, but no wave with less than ~2 steps of S slots unless the panel has
 // many pattern segments (a wave runs its segments one after another, each a
@@ -678,6 +873,25 @@ int launch(const sc_plan *p, const sc_gen_record *rec, sc_gen_launch_fn fn, cons
   return SC_OK;
 }
 
+// The band kernel when the plan has a band layout and N fits it; false
+// otherwise.  work / counters: the split-K workspace to use (work_cap floats).
+bool launch_band(const sc_plan *p, const float *B, float *C, int32_t N, int32_t flags, void *stream, float *work,
+                 unsigned *counters, size_t work_cap) {
+  if (!p->band.img) return false;
+  const sc::BandGeometry g = sc::band_geometry(p->band, N, sc::kBandTargetUnits, work_cap);
+  if (!g.use) return false;
+  if (!B || !C) throw sc::Error{SC_ERR_ARG, "null device buffer"};
+  int dev = -1;
+  hip_check(hipGetDevice(&dev), "hipGetDevice");
+  if (dev != p->device) throw sc::Error{SC_ERR_ARG, "plan lives on another device than the current one"};
+  if ((uintptr_t)B % 16 || (uintptr_t)C % 16)
+    throw sc::Error{SC_ERR_ARG, "B and C must be aligned to their vector width (16 B when N % 4 == 0)"};
+  hip_check(sc::launch_band(p->band, g, B, C, work, counters, p->M, p->K, N, (flags & SC_ACCUMULATE) ? 1 : 0,
+                            (hipStream_t)stream),
+            "band kernel launch");
+  return true;
+}
+
 }  // namespace
 
 extern "C" {
@@ -686,12 +900,14 @@ int sc_plan_create(const sc_cfmtx *cf, int32_t flags, sc_plan **out) {
   SC_GUARD([&] {
     if (!cf || !out) throw sc::Error{SC_ERR_ARG, "null argument"};
     if (flags & ~(SC_PLAN_DROP_PADDING | SC_PLAN_TILED | SC_PLAN_CHUNKED | SC_PLAN_F16_VALUES | SC_PLAN_ROWS |
-                  SC_PLAN_PATTERNS))
+                  SC_PLAN_PATTERNS | SC_PLAN_BANDS))
       throw sc::Error{SC_ERR_ARG, "unknown plan flags"};
     if ((flags & SC_PLAN_ROWS) && (flags & SC_PLAN_PATTERNS))
       throw sc::Error{SC_ERR_ARG, "SC_PLAN_ROWS and SC_PLAN_PATTERNS are exclusive"};
     if ((flags & SC_PLAN_TILED) && (flags & SC_PLAN_CHUNKED))
       throw sc::Error{SC_ERR_ARG, "SC_PLAN_TILED and SC_PLAN_CHUNKED are exclusive"};
+    if ((flags & SC_PLAN_BANDS) && (flags & SC_PLAN_ROWS))
+      throw sc::Error{SC_ERR_ARG, "SC_PLAN_BANDS needs the kernel_m 4 panels (not SC_PLAN_ROWS)"};
     *out = create_plan(sc_cfmtx_ref(cf), flags);
   });
 }
@@ -714,8 +930,17 @@ int sc_plan_describe(const sc_plan *p, int32_t N, char *buf, size_t buflen) {
   SC_GUARD([&] {
     if (!p || !buf || buflen == 0) throw sc::Error{SC_ERR_ARG, "null argument"};
     if (N < 1) throw sc::Error{SC_ERR_ARG, "N must be >= 1"};
-    p = layout_for(p, N);
     std::string d;
+    const sc::BandGeometry bg = sc::band_geometry(p->band, N);
+    if (bg.use) {
+      d = "band_kernel km=4 cols=" + std::to_string(sc::kBandCols) + " tile_rows=" + std::to_string(p->band.KT) +
+          " bands=" + std::to_string(p->band.nbands) + " chunks=" + std::to_string(bg.nch) + " ks=" +
+          std::to_string(bg.nks) + " tiles_per_unit=" + std::to_string(bg.tpu) + " grid=" + std::to_string(bg.grid);
+      if (d.size() + 1 > buflen) throw sc::Error{SC_ERR_ARG, "buffer too small"};
+      std::memcpy(buf, d.c_str(), d.size() + 1);
+      return;
+    }
+    p = layout_for(p, N);
     const sc::TileGeometry tg = sc::tile_geometry(p->view, N);
     const sc::ChunkGeometry cg = sc::chunk_geometry(p->view, N);
     if (!tg.use && cg.use) {
@@ -755,6 +980,9 @@ int sc_spmm(const sc_plan *plan, const float *dB, float *dC, int32_t N, int32_t 
   SC_GUARD([&] {
     if (flags & ~SC_ACCUMULATE) throw sc::Error{SC_ERR_ARG, "unknown flags"};
     if (!plan) throw sc::Error{SC_ERR_ARG, "null plan"};
+    if (N >= 1 && launch_band(plan, dB, dC, N, flags, hip_stream, plan->band_work, plan->band_cnt,
+                              sc::kBandWorkFloats))
+      return;
     if (N >= 1) plan = layout_for(plan, N);
     launch(plan, plan->gen.rec, (sc_gen_launch_fn)plan->gen.launch, dB, dC, N, flags, waves_per_panel, hip_stream);
   });
@@ -815,6 +1043,9 @@ void sc_plan_destroy(sc_plan *plan) {
   if (plan->dmem) (void)hipFree(plan->dmem);
   if (plan->work) (void)hipFree(plan->work);
   if (plan->tcount) (void)hipFree(plan->tcount);
+  if (plan->band_mem) (void)hipFree(plan->band_mem);
+  if (plan->band_work) (void)hipFree(plan->band_work);
+  if (plan->band_cnt) (void)hipFree(plan->band_cnt);
   delete plan;
 }
 

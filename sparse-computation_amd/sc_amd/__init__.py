@@ -7,7 +7,7 @@ once) with ``spmm`` / ``spmv`` on torch tensors.  All work is done by
 ``lib/libsc.so``; nothing here computes a result itself.
 """
 from ._lib import EXPORTS, LIB_PATH, LibscError, lib  # noqa: F401
-from .device import (ACCUMULATE, PLAN_CHUNKED, PLAN_DROP_PADDING, PLAN_F16_VALUES,  # noqa: F401
+from .device import (ACCUMULATE, PLAN_BANDS, PLAN_CHUNKED, PLAN_DROP_PADDING, PLAN_F16_VALUES,  # noqa: F401
                      PLAN_PATTERNS, PLAN_ROWS, PLAN_TILED, GeneratedUnit, Plan)
 from .format import (MTX_SCIPY, MTX_SYMLIB, VALUES_INTEGER, VALUES_PATTERN,  # noqa: F401
                      VALUES_REAL, Cfmtx, Csr, companion_mtx_path, load_cfmtx_matrices,

@@ -15,6 +15,7 @@ PLAN_CHUNKED = 4
 PLAN_F16_VALUES = 8
 PLAN_ROWS = 16
 PLAN_PATTERNS = 32
+PLAN_BANDS = 64
 ACCUMULATE = 1
 
 
