@@ -54,6 +54,8 @@ constexpr size_t kBandLdsBytes = 160 * 1024;
 constexpr int kBandTargetUnits = 256;
 constexpr size_t kBandWorkFloats = (size_t)kBandTargetUnits * kBandRows * kBandCols;
 constexpr size_t kBandCounters = kBandTargetUnits;
+static_assert(kBandWorkFloats == kSplitWorkFloats && kBandCounters <= kSplitCounters,
+              "the band kernel's split K fits the plan workspace");
 
 // Wave image (dwords), one per (band, K tile, wave), 16-byte aligned:
 //   [0], [1]  dense items of panels 0 and 1 (nd0, nd1)

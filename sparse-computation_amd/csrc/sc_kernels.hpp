@@ -1391,7 +1391,16 @@ struct TileGeometry {
   long long counters = 0;     // one per (row block, chunk) when nks > 1
 };
 
-inline TileGeometry tile_geometry(const DevView &v, int N) {
+// Split-K workspace of a plan (allocated with the plan, so no launch
+// allocates): partial sums and arrival counters.  The tiled and band kernels
+// size their K split to fit it.
+constexpr size_t kSplitWorkFloats = (size_t)256 * 128 * 64;  // 8 MiB
+constexpr size_t kSplitCounters = 4096;
+
+// work_cap / counter_cap: the workspace the launch will pass (floats,
+// counters); the K split shrinks until its partial sums fit.
+inline TileGeometry tile_geometry(const DevView &v, int N, size_t work_cap = kSplitWorkFloats,
+                                  size_t counter_cap = kSplitCounters) {
   TileGeometry t;
   if (!v.timg || v.kblock_kind != 1 || v.tkb != kTileRows || v.tppb != kTilePanels || N % 64 != 0 ||
       v.npanels <= 0 || v.tnkb <= 0 || v.tchunk_dw > 4 * 64 * kTilePanels)
@@ -1410,12 +1419,15 @@ inline TileGeometry tile_geometry(const DevView &v, int N) {
   const long long target = t.lds * 2 <= kLdsBytes ? 512 : 256;
   const long long rbc = (long long)v.tnrb * t.chunks;
   int nks = (int)std::max<long long>(1, std::min<long long>(v.tnkb, (target + rbc / 2) / rbc));
-  nks = std::max(nks, (v.tnkb + kTileMaxPerUnit - 1) / kTileMaxPerUnit);
+  const int nks_min = (v.tnkb + kTileMaxPerUnit - 1) / kTileMaxPerUnit;
+  while (nks > std::max(1, nks_min) && (size_t)nks * v.M * N > work_cap) --nks;
+  nks = std::max(nks, nks_min);
   t.tpu = (v.tnkb + nks - 1) / nks;
   t.nks = (v.tnkb + t.tpu - 1) / t.tpu;
   t.work_floats = t.nks > 1 ? (long long)t.nks * v.M * N : 0;
   t.counters = t.nks > 1 ? rbc : 0;
   if (t.work_floats * (long long)sizeof(float) >= (1ll << 31)) t.use = false;  // buffer offsets
+  if ((size_t)t.work_floats > work_cap || (size_t)t.counters > counter_cap) t.use = false;
   return t;
 }
 // Floats per lane of the wide path for N columns, 0 if N does not fit it.

@@ -83,14 +83,13 @@ struct sc_plan {
   sc_plan *rows = nullptr;
   std::vector<uint32_t> masks;  // row masks of the patterns holding slots
   void *dmem = nullptr;  // one allocation holding every array
-  // split-K partial sums of the tiled kernel: grown on the first call that
-  // needs more (so that call must not be inside a HIP graph capture)
-  mutable float *work = nullptr;
-  mutable long long work_floats = 0;
-  // arrival counters of the split-K units (zeroed when allocated; every
-  // launch leaves them at zero)
-  mutable unsigned *tcount = nullptr;
-  mutable long long tcount_n = 0;
+  // split-K partial sums and arrival counters of the tiled kernel
+  // (SC_PLAN_TILED), allocated with the plan (kSplitWorkFloats floats,
+  // kSplitCounters counters, zeroed; every launch leaves the counters at zero)
+  float *work = nullptr;
+  long long work_floats = 0;
+  unsigned *tcount = nullptr;
+  long long tcount_n = 0;
   sc::DevView view{};
   GenEntry gen{};
   // The band layout of a kernel_m 4 plan (SC_PLAN_BANDS): wave images in
@@ -593,6 +592,14 @@ sc_plan *build_plan(const sc::Cfmtx &cf, int32_t flags, const std::vector<PatInf
   plan->view.a_bytes = 4ll * ((long long)cols.size() + (long long)vals.size());
   plan->view.vals16 = vals16.empty() ? nullptr : (const _Float16 *)(base + off_v16);
   plan->view.row_len = row_len.empty() ? nullptr : (const int *)(base + off_rowlen);
+  if (plan->view.timg) {
+    hip_check(hipMalloc((void **)&plan->work, sc::kSplitWorkFloats * sizeof(float)), "hipMalloc(split-K workspace)");
+    plan->work_floats = (long long)sc::kSplitWorkFloats;
+    hip_check(hipMalloc((void **)&plan->tcount, sc::kSplitCounters * sizeof(unsigned)), "hipMalloc(split-K counters)");
+    hip_check(hipMemset(plan->tcount, 0, sc::kSplitCounters * sizeof(unsigned)), "hipMemset(split-K counters)");
+    hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize(split-K workspace)");
+    plan->tcount_n = (long long)sc::kSplitCounters;
+  }
   return plan.release();
 }
 
@@ -846,24 +853,7 @@ int launch(const sc_plan *p, const sc_gen_record *rec, sc_gen_launch_fn fn, cons
                                    p->nslots / std::max(1, p->npanels)).lds > 65536)
     throw sc::Error{SC_ERR_ARG, "too many waves per panel for this N"};
   sc::DevView view = p->view;
-  const sc::TileGeometry tg = sc::tile_geometry(view, N);
-  if (tg.use && tg.work_floats > p->work_floats) {
-    if (p->work) (void)hipFree(p->work);
-    p->work = nullptr;
-    p->work_floats = 0;
-    hip_check(hipMalloc((void **)&p->work, (size_t)tg.work_floats * sizeof(float)),
-              "hipMalloc(split-K workspace)");
-    p->work_floats = tg.work_floats;
-  }
-  if (tg.use && tg.counters > p->tcount_n) {
-    if (p->tcount) (void)hipFree(p->tcount);
-    p->tcount = nullptr;
-    p->tcount_n = 0;
-    hip_check(hipMalloc((void **)&p->tcount, (size_t)tg.counters * sizeof(unsigned)),
-              "hipMalloc(split-K counters)");
-    hip_check(hipMemset(p->tcount, 0, (size_t)tg.counters * sizeof(unsigned)), "hipMemset(split-K counters)");
-    p->tcount_n = tg.counters;
-  }
+  // the split-K workspace, allocated with the plan (nothing is allocated here)
   view.work = p->work;
   view.work_floats = p->work_floats;
   view.tcount = p->tcount;

@@ -343,3 +343,26 @@ def test_small_n_gather_kernel_generated_pack_unit(n):
     C = plan.spmm_generated(unit, torch.from_numpy(B).to(DEV))
     torch.cuda.synchronize()
     assert oracle_check(A, B, C.cpu().numpy())[0] <= REL_TOL
+
+
+def test_tiled_first_launch_captured_in_a_graph():
+    # a tiled plan owns its split-K workspace from creation: its very first
+    # launch may sit inside a HIP graph capture (no allocation in the launch)
+    A, B = synth_case(1000, 700, 0.2, 128, seed=0x5EED0000 + 7500)
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1), sc_amd.PLAN_TILED)
+    assert plan.describe(128).startswith("tiled_kernel"), plan.describe(128)
+    Bt = torch.from_numpy(B).to(DEV)
+    Ct = torch.full((1000, 128), float("nan"), device=DEV)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        plan.spmm(Bt, Ct)
+    ref = None
+    for i in range(3):
+        Ct.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        C = Ct.cpu().numpy()
+        assert oracle_check(A, B, C)[0] <= REL_TOL, i
+        ref = C if ref is None else ref
+        assert np.array_equal(C, ref), i
