@@ -162,6 +162,19 @@ int sc_plan_describe(const sc_plan *plan, int32_t N, char *buf, size_t buflen);
 #define SC_ACCUMULATE 1
 int sc_spmm(const sc_plan *plan, const float *dB, float *dC, int32_t N, int32_t flags,
             int32_t waves_per_panel, void *hip_stream);
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  sc_spmm with the split-K kernels' partial sums and
+ * arrival counters (SC_PLAN_BANDS, SC_PLAN_TILED) in the library's static
+ * per-device scratch instead of the plan's workspace; allocates nothing.
+ * The scratch is 8 MiB of partial sums plus 16 KiB of counters, held on each
+ * GPU the library runs on until the process ends; the K split is sized to
+ * fit it (as the plan's workspace, so results equal sc_spmm's), and a launch
+ * that would need more is refused with SC_ERR_UNSUPPORTED.  Every call on one
+ * GPU shares that GPU's scratch: calls that overlap on one GPU (other
+ * streams, other threads) race. */
+int sc_spmm_noalloc(const sc_plan *plan, const float *dB, float *dC, int32_t N, int32_t flags,
+                    int32_t waves_per_panel, void *hip_stream);
 /* y = A*x (N = 1). */
 int sc_spmv(const sc_plan *plan, const float *dx, float *dy, int32_t flags, void *hip_stream);
 /* The binary16 small-B path: C = A*B with A's values (the plan's binary16

@@ -18,6 +18,7 @@
 #include <array>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -834,8 +835,28 @@ void check_record(const sc_plan *p, const sc_gen_record *rec, int32_t N) {
   }
 }
 
+// A workspace the caller brings for the split-K kernels, in place of the
+// plan's own (sc_spmm_noalloc: the library's static scratch).
+struct Scratch {
+  float *work;
+  size_t work_floats;
+  unsigned *counters;
+  size_t counters_n;
+};
+
+__global__ void zero_counters(unsigned *c, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) c[i] = 0u;
+}
+
+// Arrival counters must start at zero: a small fill kernel, not a memset, so
+// the call stays capturable in a HIP graph.
+void clear_counters(unsigned *c, size_t n, hipStream_t stream) {
+  hipLaunchKernelGGL(zero_counters, dim3(1), dim3(256), 0, stream, c, (int)n);
+  hip_check(hipGetLastError(), "counter clear launch");
+}
+
 int launch(const sc_plan *p, const sc_gen_record *rec, sc_gen_launch_fn fn, const float *B, float *C,
-           int32_t N, int32_t flags, int32_t waves, void *stream) {
+           int32_t N, int32_t flags, int32_t waves, void *stream, const Scratch *scratch = nullptr) {
   if (!p) throw sc::Error{SC_ERR_ARG, "null plan"};
   if (!fn) throw sc::Error{SC_ERR_ARG, "null generated-kernel launcher"};
   if (N < 1) throw sc::Error{SC_ERR_ARG, "N must be >= 1"};
@@ -853,11 +874,16 @@ int launch(const sc_plan *p, const sc_gen_record *rec, sc_gen_launch_fn fn, cons
                                    p->nslots / std::max(1, p->npanels)).lds > 65536)
     throw sc::Error{SC_ERR_ARG, "too many waves per panel for this N"};
   sc::DevView view = p->view;
-  // the split-K workspace, allocated with the plan (nothing is allocated here)
-  view.work = p->work;
-  view.work_floats = p->work_floats;
-  view.tcount = p->tcount;
-  view.tcount_n = p->tcount_n;
+  // the split-K workspace: the plan's, or the caller's scratch (nothing is
+  // allocated here)
+  view.work = scratch ? scratch->work : p->work;
+  view.work_floats = scratch ? (long long)scratch->work_floats : p->work_floats;
+  view.tcount = scratch ? scratch->counters : p->tcount;
+  view.tcount_n = scratch ? (long long)scratch->counters_n : p->tcount_n;
+  if (scratch) {
+    const sc::TileGeometry tg = sc::tile_geometry(view, N);
+    if (tg.use && tg.nks > 1) clear_counters(scratch->counters, (size_t)tg.counters, (hipStream_t)stream);
+  }
   int e = fn(&view, B, C, N, (flags & SC_ACCUMULATE) ? 1 : 0, w, stream);
   hip_check((hipError_t)e, "pattern kernel launch");
   return SC_OK;
@@ -866,10 +892,11 @@ int launch(const sc_plan *p, const sc_gen_record *rec, sc_gen_launch_fn fn, cons
 // The band kernel when the plan has a band layout and N fits it; false
 // otherwise.  work / counters: the split-K workspace to use (work_cap floats).
 bool launch_band(const sc_plan *p, const float *B, float *C, int32_t N, int32_t flags, void *stream, float *work,
-                 unsigned *counters, size_t work_cap) {
+                 unsigned *counters, size_t work_cap, bool clear = false) {
   if (!p->band.img) return false;
   const sc::BandGeometry g = sc::band_geometry(p->band, N, sc::kBandTargetUnits, work_cap);
   if (!g.use) return false;
+  if (clear && g.nks > 1) clear_counters(counters, (size_t)g.counters, (hipStream_t)stream);
   if (!B || !C) throw sc::Error{SC_ERR_ARG, "null device buffer"};
   int dev = -1;
   hip_check(hipGetDevice(&dev), "hipGetDevice");
@@ -880,6 +907,39 @@ bool launch_band(const sc_plan *p, const float *B, float *C, int32_t N, int32_t 
                             (hipStream_t)stream),
             "band kernel launch");
   return true;
+}
+
+// ---- the static scratch of sc_spmm_noalloc --------------------------------
+constexpr size_t kScratchWorkBytes = sc::kSplitWorkFloats * sizeof(float);
+constexpr size_t kScratchBytes = kScratchWorkBytes + sc::kSplitCounters * sizeof(unsigned);
+
+}  // namespace
+
+// The split-K partial sums and arrival counters of sc_spmm_noalloc: one copy
+// on every GPU the library runs on, held until the process ends.  In host
+// code `scratch` names a host-side stand-in, not device memory: host code uses
+// only the device address that hipGetSymbolAddress returns for the current
+// device (scratch_base).
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char *g_scratch_base[kMaxDevices] = {};
+
+// Device address of `scratch` on device dev, which must be current: looked up
+// with hipGetSymbolAddress on the first call on that device, then kept.
+unsigned char *scratch_base(int dev) {
+  if (dev < 0 || dev >= kMaxDevices) throw sc::Error{SC_ERR_UNSUPPORTED, "device index beyond the scratch table"};
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_base[dev]) {
+    void *ptr = nullptr;
+    hip_check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (!ptr) throw sc::Error{SC_ERR_HIP, "hipGetSymbolAddress(scratch) returned a null address"};
+    g_scratch_base[dev] = (unsigned char *)ptr;
+  }
+  return g_scratch_base[dev];
 }
 
 }  // namespace
@@ -975,6 +1035,33 @@ int sc_spmm(const sc_plan *plan, const float *dB, float *dC, int32_t N, int32_t 
       return;
     if (N >= 1) plan = layout_for(plan, N);
     launch(plan, plan->gen.rec, (sc_gen_launch_fn)plan->gen.launch, dB, dC, N, flags, waves_per_panel, hip_stream);
+  });
+}
+
+int sc_spmm_noalloc(const sc_plan *plan, const float *dB, float *dC, int32_t N, int32_t flags,
+                    int32_t waves_per_panel, void *hip_stream) {
+  SC_GUARD([&] {
+    if (flags & ~SC_ACCUMULATE) throw sc::Error{SC_ERR_ARG, "unknown flags"};
+    if (!plan) throw sc::Error{SC_ERR_ARG, "null plan"};
+    int dev = -1;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev != plan->device) throw sc::Error{SC_ERR_ARG, "plan lives on another device than the current one"};
+    unsigned char *base = scratch_base(dev);
+    const Scratch sc{(float *)base, sc::kSplitWorkFloats, (unsigned *)(base + kScratchWorkBytes), sc::kSplitCounters};
+    // the split-K kernels size their K split to fit this scratch (the plan
+    // workspace has the same size, so the launches match sc_spmm's); a
+    // geometry that needed more would be refused here
+    if (N >= 1 && plan->band.img) {
+      const sc::BandGeometry g = sc::band_geometry(plan->band, N, sc::kBandTargetUnits, sc.work_floats);
+      if (g.use && (g.work_floats > sc.work_floats || (size_t)g.counters > sc.counters_n))
+        throw sc::Error{SC_ERR_UNSUPPORTED, "the band kernel would need more than the " +
+                                                std::to_string(kScratchBytes) + "-byte static scratch"};
+    }
+    if (N >= 1 && launch_band(plan, dB, dC, N, flags, hip_stream, sc.work, sc.counters, sc.work_floats, true))
+      return;
+    if (N >= 1) plan = layout_for(plan, N);
+    launch(plan, plan->gen.rec, (sc_gen_launch_fn)plan->gen.launch, dB, dC, N, flags, waves_per_panel, hip_stream,
+           &sc);
   });
 }
 

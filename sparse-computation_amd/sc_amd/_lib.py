@@ -50,6 +50,7 @@ _SIGS = {
     "sc_plan_create": ([vp, i32, C.POINTER(vp)], C.c_int),
     "sc_plan_info": ([vp, i32p, i32p, i32p, i32p, i64p, i64p, i64p], C.c_int),
     "sc_spmm": ([vp, vp, vp, i32, i32, i32, vp], C.c_int),
+    "sc_spmm_noalloc": ([vp, vp, vp, i32, i32, i32, vp], C.c_int),
     "sc_spmv": ([vp, vp, vp, i32, vp], C.c_int),
     "sc_spmm_f16": ([vp, vp, vp, i32, i32, i32, vp], C.c_int),
     "sc_plan_destroy": ([vp], None),

@@ -103,6 +103,18 @@ class Plan:
                             ACCUMULATE if accumulate else 0, waves, _stream_handle(stream)))
         return C_out
 
+    def spmm_noalloc(self, B, C_out, accumulate=False, waves=0, stream=None):
+        """C = A @ B through sc_spmm_noalloc: the split-K kernels use the
+        library's static per-device scratch, nothing is allocated (C_out must
+        be given)."""
+        info = self.info()
+        N = B.shape[1] if B.dim() == 2 else 1
+        self._check_operand(B, info["n"], N, "B")
+        self._check_operand(C_out, info["m"], N, "C")
+        check(lib().sc_spmm_noalloc(self._h, C.c_void_p(B.data_ptr()), C.c_void_p(C_out.data_ptr()), N,
+                                    ACCUMULATE if accumulate else 0, waves, _stream_handle(stream)))
+        return C_out
+
     def spmm_ptr(self, b_ptr: int, c_ptr: int, N: int, flags: int = 0, waves: int = 0,
                  stream=None) -> None:
         """Raw-pointer form (no shape checks): for timing loops."""
