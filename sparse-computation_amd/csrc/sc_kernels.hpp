@@ -18,7 +18,8 @@
 //   * per lane the C tile is acc[KM][V] in VGPRs; a pattern body adds
 //     value(slot,row) * B[col(slot), c0 .. c0+V) into the rows of its mask
 //     only, with the row indices compile-time constants;
-//   * the S slot sub-lanes are reduced with a butterfly of cross-lane moves,
+//   * the S slot sub-lanes are reduced into the first lanes with DPP row
+//     shifts and the gfx950 lane swaps (v_permlane16_swap, v_permlane32_swap),
 //     then the W waves through LDS in a fixed order, so results are
 //     deterministic run to run.
 #pragma once
@@ -274,15 +275,50 @@ __device__ __forceinline__ void fma_row(float (&acc)[V], float v, const float (&
   for (int e = 0; e < V; ++e) acc[e] = __builtin_fmaf(v, b[e], acc[e]);
 }
 
-// Cross-lane sum over the S slot sub-lanes (lanes g, g+L, g+2L, ...).
+// The value of lane l + OFF (OFF a power of two up to 32) for the lanes a
+// reduction into the low lanes reads, without an LDS round trip:
+//   OFF < 16: a DPP row shift (row_shl: lane l reads lane l + OFF of its row of
+//             16; the add it feeds takes the DPP operand directly);
+//   OFF = 16: v_permlane16_swap (rows 0 and 2 read rows 1 and 3);
+//   OFF = 32: v_permlane32_swap (lanes 0..31 read lanes 32..63).
+// The lane swaps are written as inline asm: with only the second result of
+// __builtin_amdgcn_permlane{16,32}_swap used, the compiler of this image read
+// the first one (measured: sums came out wrong), while the instruction itself
+// behaves as documented (rows 1 and 3 of the second operand end in rows 0 and
+// 2 of it; checked lane by lane on MI355X).  The s_nop covers the wait the
+// compiler itself places between a VALU write and these instructions.
+template <int OFF>
+__device__ __forceinline__ float lane_down(float x) {
+  static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8 || OFF == 16 || OFF == 32, "power of two up to 32");
+  unsigned a = __builtin_bit_cast(unsigned, x), b = a;
+  if constexpr (OFF < 16) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, (int)a, 0x100 + OFF, 0xf, 0xf, true));
+  } else if constexpr (OFF == 16) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return __builtin_bit_cast(float, b);
+  } else {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return __builtin_bit_cast(float, b);
+  }
+}
+
+// Sum of the S slot sub-lanes (lanes g, g+L, g+2L, ..., L a power of two) into
+// lanes 0..L-1, in the pairing order of a butterfly (offsets L, 2L, ..., 32);
+// the other lanes are left with partial sums.
 template <int KM, int V>
 __device__ __forceinline__ void reduce_slot_lanes(float (&acc)[KM][V], int L) {
-  for (int off = L; off < 64; off <<= 1) {
-#pragma unroll
-    for (int r = 0; r < KM; ++r)
-#pragma unroll
-      for (int e = 0; e < V; ++e) acc[r][e] += __shfl_xor(acc[r][e], off, 64);
+#define SC_REDUCE_STEP(OFF)                                                      \
+  if (L <= OFF) {                                                                \
+    _Pragma("unroll") for (int r = 0; r < KM; ++r)                               \
+      _Pragma("unroll") for (int e = 0; e < V; ++e) acc[r][e] += lane_down<OFF>(acc[r][e]); \
   }
+  SC_REDUCE_STEP(1)
+  SC_REDUCE_STEP(2)
+  SC_REDUCE_STEP(4)
+  SC_REDUCE_STEP(8)
+  SC_REDUCE_STEP(16)
+  SC_REDUCE_STEP(32)
+#undef SC_REDUCE_STEP
 }
 
 template <int V>
@@ -1519,7 +1555,7 @@ inline Geometry geometry(int km, int N, int W, long long K = 0, int max_pslots =
 // and values with one 16-byte load each (every panel starts on a 16-byte
 // boundary), gathers their four B rows (N floats each, one 4-, 8- or 16-byte
 // load) and accumulates; slots past the row's last one are masked, never read
-// from B; the wave reduces with a butterfly of shuffles.  The shortest
+// from B; the wave reduces into lane 0 with lane swaps and DPP row shifts.  The shortest
 // dependent chain a row has: its offsets, its stream, B, the store.
 // Measured on MI355X against the lanes-over-slots kernel (graph replay): SpMV
 // 512^2 at 70 % sparsity 2.92 -> 2.23 us, small-B 512^2 N = 1 (rows of km 4)
@@ -1588,10 +1624,16 @@ __global__ void __launch_bounds__(64 * ROWS)
       if (e + 3 < n) acc[k] = __builtin_fmaf(v.w, b3[k], acc[k]);
     }
   }
+  // the wave's sum into lane 0 (same pairings as a butterfly of offsets 32 .. 1)
 #pragma unroll
-  for (int k = 0; k < V; ++k)
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) acc[k] += __shfl_xor(acc[k], o);
+  for (int k = 0; k < V; ++k) {
+    acc[k] += lane_down<32>(acc[k]);
+    acc[k] += lane_down<16>(acc[k]);
+    acc[k] += lane_down<8>(acc[k]);
+    acc[k] += lane_down<4>(acc[k]);
+    acc[k] += lane_down<2>(acc[k]);
+    acc[k] += lane_down<1>(acc[k]);
+  }
   if (lane == 0) {
     float *dst = C + (size_t)row * V;
     // a branch, not a select: C is read only when accumulating (a select
