@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SC_ABI_VERSION 1
+#define SC_ABI_VERSION 2
 
 /* status codes */
 #define SC_OK 0
@@ -191,6 +191,10 @@ void sc_plan_destroy(sc_plan *plan);
 
 /* ------------------------------------------------------- generated kernels */
 
+/* sc_gen_<name>_launch of a generated unit. */
+typedef int (*sc_gen_launch_fn)(const void *view, const float *B, float *C, int N, int accumulate,
+                                int waves, void *hip_stream);
+
 /* Parameters a generated kernel unit was emitted with by code_gen/main_spmm.py,
  * main_spmm_small_b_col.py or main_spmv.py (exported as sc_gen_<name>_record).
  * The reference bakes the same parameters into its generated headers
@@ -203,16 +207,18 @@ typedef struct sc_gen_record {
   int32_t npatterns;      /* number of pattern bodies                          */
   int32_t variant;        /* 0 = any N, otherwise the only N accepted          */
   const uint32_t *masks;  /* row mask of each body (bit r = panel row r)       */
+  /* sc_gen_<name>_launch_rows: the unit's kernel_m 1 body on a plan's one-row
+   * layout of the same slots, or NULL */
+  sc_gen_launch_fn rows_launch;
 } sc_gen_record;
-
-/* sc_gen_<name>_launch of a generated unit. */
-typedef int (*sc_gen_launch_fn)(const void *view, const float *B, float *C, int N, int accumulate,
-                                int waves, void *hip_stream);
 
 /* Launch a generated unit on a plan after checking that the unit fits it:
  * same km, a pack that divides every segment, a body for every pattern the
- * plan holds and, for fixed-N units, the same N.  Replaces the launch in the
- * generated classes' execute() (spmm_demo_gpu_utils.h:1700-1720). */
+ * plan holds and, for fixed-N units, the same N.  A plan that holds the
+ * one-row layout too (created without SC_PLAN_PATTERNS) runs under sc_spmm's
+ * rule: launches whose one-row B gathers stay under 128 MiB run the unit's
+ * kernel_m 1 body (rec->rows_launch) on that layout.  Replaces the launch in
+ * the generated classes' execute() (spmm_demo_gpu_utils.h:1700-1720). */
 int sc_spmm_generated(const sc_plan *plan, const sc_gen_record *rec, sc_gen_launch_fn launch,
                       const float *dB, float *dC, int32_t N, int32_t flags,
                       int32_t waves_per_panel, void *hip_stream);

@@ -426,6 +426,54 @@ def _emit_seg_chain(usable, name, targs, call):
     return out
 
 
+def _emit_dispatch(usable, km):
+    """The dispatcher struct of a set of bodies (run_tile, run_segs, run_wide, run)."""
+    out = ["struct dispatch {"]
+    out += _emit_tile_chain(usable, lambda bits: f"{tile_name(bits)}<V>(acc, a);")
+    out += _emit_seg_chain(usable, "run_segs", "int KM, int V, class A",
+                           lambda bits: f"{body_name(bits)}<V, A>(acc, a);")
+    out.append("  template <int KM, int V>")
+    out.append("  __device__ __forceinline__ static void run_wide(int mask, float (&acc)[KM][V], "
+               "const sc::WideArgs &a) {")
+    out.append("    switch (mask) {")
+    for bits, pid in usable:
+        out.append(f"      case {_mask(bits)}: {wide_name(bits)}<V>(acc, a); break;  // id {pid}")
+    out.append("      default: break;")
+    out.append("    }")
+    out.append("  }")
+    out.append("  template <int KM, int V, class A>")
+    out.append("  __device__ __forceinline__ static void run(int mask, float (&acc)[KM][V], "
+               "const A &a) {")
+    out.append(f"    static_assert(KM == {km}, \"dispatcher generated for km={km}\");")
+    out.append("    switch (mask) {")
+    for bits, pid in usable:
+        out.append(f"      case {_mask(bits)}: {body_name(bits)}<V, A>(acc, a); break;  // id {pid}")
+    out.append("      default: break;")
+    out.append("    }")
+    out.append("  }")
+    out.append("};")
+    return out
+
+
+def _emit_rows_namespace():
+    """The one-row (km = 1) bodies every unit carries: plans hold the same
+    slots re-laid as one-row panels, and sc_spmm_generated runs them on that
+    layout under the rule sc_spmm follows (small launches, where one
+    workgroup per row beats the km-row panels' longer chains)."""
+    usable = [("1", 0)]
+    out = ["// one-row bodies: the same slots as one-row panels (kernel_m 1)",
+           "namespace rows {", ""]
+    out.append(emit_body(1, "1", 0, 1, 4))
+    out.append("")
+    out.append(emit_wide_body(1, "1", 0, 1))
+    out.append("")
+    out.append(emit_tile_body(1, "1", 0))
+    out.append("")
+    out += _emit_dispatch(usable, 1)
+    out += ["", "}  // namespace rows", ""]
+    return out
+
+
 def sanitize(name: str) -> str:
     return re.sub(r"[^0-9A-Za-z_]", "_", name)
 
@@ -501,7 +549,7 @@ def emit_unit(name: str, km: int, patterns, kn: int = 1, waves: int = 0, variant
         out.append("")
         out.append(f"}}  // namespace sc_gen_{name}")
         out.append("")
-        return _emit_exports(out, name, km, kn, waves, variant, usable, alias)
+        return _emit_exports(out, name, km, kn, waves, variant, usable, alias, rows=False)
     for bits, pid in usable:
         out.append(emit_body(km, bits, pid, kn, unroll))
         out.append("")
@@ -509,6 +557,7 @@ def emit_unit(name: str, km: int, patterns, kn: int = 1, waves: int = 0, variant
         out.append("")
         out.append(emit_tile_body(km, bits, pid))
         out.append("")
+    out += _emit_rows_namespace()
     out.append("struct dispatch {")
     out += _emit_tile_chain(usable, lambda bits: f"{tile_name(bits)}<V>(acc, a);")
     out += _emit_seg_chain(usable, "run_segs", "int KM, int V, class A",
@@ -539,14 +588,32 @@ def emit_unit(name: str, km: int, patterns, kn: int = 1, waves: int = 0, variant
     return _emit_exports(out, name, km, kn, waves, variant, usable, alias)
 
 
-def _emit_exports(out, name, km, kn, waves, variant, usable, alias):
-    """The unit's extern "C" record, masks, launcher and optional alias."""
+def _emit_exports(out, name, km, kn, waves, variant, usable, alias, rows=True):
+    """The unit's extern "C" record, masks, launcher(s) and optional alias."""
     masks = ", ".join(f"{_mask(b)}u" for b, _ in usable) or "0u"
     out.append(f'extern "C" __attribute__((visibility("default"))) const uint32_t '
                f"sc_gen_{name}_masks[] = {{{masks}}};")
-    out.append(f'extern "C" __attribute__((visibility("default"))) const sc_gen_record '
+    if rows:
+        # the one-row launcher: the same unit's km = 1 body on a plan's one-row layout
+        out.append(f'extern "C" __attribute__((visibility("default"))) hipError_t '
+                   f"sc_gen_{name}_launch_rows(const sc::DevView *v, const float *B, float *C, int N,")
+        out.append("                                              int accumulate, int waves, "
+                   "hipStream_t stream) {")
+        if variant:
+            out.append(f"  if (N != {variant}) return hipErrorInvalidValue;")
+        out.append("  if (waves <= 0) waves = 1;")
+        out.append(f"  return sc::launch_panels<1, sc_gen_{name}::rows::dispatch>(*v, B, C, N, accumulate, "
+                   "waves, 1, stream);")
+        out.append("}")
+    # a plain host global, its launcher pointer set at load time: a constant
+    # initializer naming a host function would also be emitted for the device
+    out.append(f'extern "C" __attribute__((visibility("default"))) sc_gen_record '
                f"sc_gen_{name}_record = {{{km}, {kn}, {waves}, {len(usable)}, {variant}, "
-               f"sc_gen_{name}_masks}};")
+               f"sc_gen_{name}_masks, nullptr}};")
+    if rows:
+        out.append(f"__attribute__((constructor)) static void sc_gen_{name}_record_init() {{")
+        out.append(f"  sc_gen_{name}_record.rows_launch = (sc_gen_launch_fn)sc_gen_{name}_launch_rows;")
+        out.append("}")
     out.append("")
     out.append(f'extern "C" __attribute__((visibility("default"))) hipError_t '
                f"sc_gen_{name}_launch(const sc::DevView *v, const float *B, float *C, int N,")

@@ -31,7 +31,7 @@ const sc::Cfmtx &sc_cfmtx_ref(const sc_cfmtx *cf);
 
 // generated units (csrc/gen/sc_gen_builtin_km*.hip)
 #define SC_DECLARE_GEN(k)                                                                        \
-  extern "C" const sc_gen_record sc_gen_builtin_km##k##_record;                                  \
+  extern "C" sc_gen_record sc_gen_builtin_km##k##_record;                                        \
   extern "C" hipError_t sc_gen_builtin_km##k##_launch(const sc::DevView *, const float *, float *, \
                                                       int, int, int, hipStream_t);               \
   extern "C" hipError_t sc_gen_builtin_km##k##_launch_f16(const sc::DevView *, const void *, void *, \
@@ -1069,6 +1069,16 @@ int sc_spmm_generated(const sc_plan *plan, const sc_gen_record *rec, sc_gen_laun
                       float *dC, int32_t N, int32_t flags, int32_t waves_per_panel, void *hip_stream) {
   SC_GUARD([&] {
     if (flags & ~SC_ACCUMULATE) throw sc::Error{SC_ERR_ARG, "unknown flags"};
+    if (!plan) throw sc::Error{SC_ERR_ARG, "null plan"};
+    if (N >= 1 && rec && rec->rows_launch && layout_for(plan, N) != plan) {
+      // the unit fits the file's layout, and its one-row body runs the same
+      // slots re-laid as one-row panels
+      check_record(plan, rec, N);
+      static const uint32_t one = 1u;
+      const sc_gen_record rows_rec = {1, 1, 0, 1, rec->variant, &one, nullptr};  // waves chosen per launch
+      launch(plan->rows, &rows_rec, rec->rows_launch, dB, dC, N, flags, waves_per_panel, hip_stream);
+      return;
+    }
     launch(plan, rec, fn, dB, dC, N, flags, waves_per_panel, hip_stream);
   });
 }

@@ -290,7 +290,9 @@ int main(int argc, char **argv) {
   };
 
   sc_plan *plan = nullptr;
-  SC_OK_OR_DIE(sc_plan_create(cf, SC_PLAN_PATTERNS, &plan));  // generated units run the pattern layout
+  // both layouts: the generated unit runs its km-row bodies or, for launches
+  // whose one-row gathers stay small, its one-row body (sc_spmm's rule)
+  SC_OK_OR_DIE(sc_plan_create(cf, 0, &plan));
   float *dB = nullptr, *dC = nullptr;
   HIP_OK(hipMalloc(&dB, B.size() * sizeof(float)));
   HIP_OK(hipMalloc(&dC, (size_t)M * N * sizeof(float)));

@@ -61,7 +61,17 @@ def test_python_reader_of_cfmtx():
 
 
 def _cases(text):
+    """Cases of the unit's main dispatch; the one-row layout's own dispatch
+    (namespace rows, a single all-ones row pattern) is left out."""
+    if "namespace rows {" in text:
+        head, rest = text.split("namespace rows {", 1)
+        text = head + rest.split("}  // namespace rows", 1)[1]
     return re.findall(r"case (\d+): pattern_(\d+)<V, A>", text)
+
+
+def _row_cases(text):
+    rows = text.split("namespace rows {", 1)[1].split("}  // namespace rows", 1)[0]
+    return re.findall(r"case (\d+): pattern_(\d+)<V, A>", rows)
 
 
 @pytest.mark.parametrize("km,kn", [(4, 1), (4, 2), (6, 3), (1, 1)])
@@ -77,6 +87,9 @@ def test_main_spmm_emits_one_body_per_pattern(tmp_path, km, kn):
         assert f"void wide_{bits}(" in text
     assert f"sc_gen_spmm_km{km}_kn{kn}_record = {{{km}, {kn}, 0, {2 ** km - 1}, 0," in text
     assert f"sc_gen_spmm_km{km}_kn{kn}_launch" in text
+    # one-row layout launcher, installed in the record at load
+    assert _row_cases(text) == [("1", "1")]
+    assert f".rows_launch = (sc_gen_launch_fn)sc_gen_spmm_km{km}_kn{kn}_launch_rows;" in text
     # a pack of kn slots is unrolled, U = max(1, 4 // kn) packs per batch: a
     # full batch of U * kn B-row loads, then a last batch of exactly the t
     # packs left (t = 1 .. U; t * kn loads that may read zeros)

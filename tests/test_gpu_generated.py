@@ -22,12 +22,27 @@ def unit(name, so_name=None):
     return sc_amd.GeneratedUnit(os.path.join(UNITS, f"libsc_unit_{so_name or name}.so"), name)
 
 
-def run(cf, u, B):
-    plan = sc_amd.Plan(cf)
+def run(cf, u, B, flags=0):
+    plan = sc_amd.Plan(cf, flags)
     Bt = torch.from_numpy(np.ascontiguousarray(B, np.float32)).to(DEV)
     C = plan.spmm_generated(u, Bt)
     torch.cuda.synchronize()
     return C.cpu().numpy()
+
+
+@pytest.mark.parametrize("n", [1, 4, 32, 128])
+def test_generated_unit_follows_the_layout_rule(n):
+    # a default plan holds both layouts: sc_spmm_generated runs the unit's
+    # one-row body where sc_spmm would run the one-row layout (all of these
+    # sizes), the km-row bodies on a SC_PLAN_PATTERNS plan; both agree with
+    # the oracle
+    A, B = synth_case(512, 512, 0.10, n, seed=0x5EED0000 + 2000 + n)
+    cf = sc_amd.Cfmtx.build(A, 4, 2)
+    assert "(rows of km=4)" in sc_amd.Plan(cf).describe(n)
+    u = unit("spmm_km4_kn2")
+    for flags in (0, sc_amd.PLAN_PATTERNS):
+        C = run(cf, u, B, flags)
+        assert oracle_check(A, B, C)[0] <= REL_TOL, (n, flags)
 
 
 @pytest.mark.parametrize("n", [1, 32, 128])
