@@ -9,21 +9,37 @@
 // LDS reads, and the L2 -> CU traffic falls to the B tiles (one copy per
 // band), the stream, and the split-K partial sums.
 //
+// Measured on MI355X (structured 4096 x 4096 at 10 % density, N = 128):
+// 33.3 us per launch against the panel kernel's 21.8, with 0.89 M L2 read
+// requests against 3.29 M.  The item loop waits on one LDS round trip per
+// step, and the split-K epilogue plus the first tile cost about 16 k cycles
+// of the unit's 64 k.  So plans build the band layout only when asked
+// (SC_PLAN_BANDS).
+//
 // Work decomposition.  A unit (workgroup of 16 waves) owns one band, one N
 // chunk of 64 columns and one range of K tiles (split K, so that the grid
 // covers the 256 CUs).  Per tile it stages B[tile rows, chunk] (256 bytes a
 // row, one extra row of zeros for padding) and each wave its own part of the
 // tile's stream (the wave image) in LDS, double-buffered for B, while the
 // waves compute the previous tile.  Wave w owns panels 2w and 2w + 1 of the
-// band.  A panel's slots in a tile come as two kinds of items:
-//   * dense items: four slots of the all-ones pattern (the 4 x 4 blocks of a
-//     km = 4 format), run on the matrix cores: v_mfma_f32_4x4x1f32 with 16
-//     blocks covers one slot's four rows times the chunk's 64 columns, lane l
-//     holding column l and register i row i of the panel;
-//   * single items: four (row, column, value) entries of one panel row, the
-//     slots of every other pattern split into their rows (a pop-2 slot gives
-//     two entries), run on the VALU with 16 lanes of 4 columns per entry.
-// Items are padded to four slots with value 0 on the zero row.
+// band.  A panel's slots in a tile, in column order, come four to an item
+// and every item runs on the matrix cores, whatever its slots' patterns
+// (rows a pattern lacks carry value 0): v_mfma_f32_4x4x1f32 has 16 blocks of
+// a 4-row by 4-column product; block b = 4s + c of an item takes slot s and
+// columns 16c + 4j + q (j the block's column, q = 0..3 over four
+// instructions), so lane 16s + 4c + j reads its slot's value for row j (the A
+// operand) with one 4-byte LDS read and the 16 bytes at column 16c + 4j of
+// the slot's B row with one 16-byte read that feeds the four instructions.
+// Each block accumulates its slot's products; the four slots' partial sums
+// (lanes 16s + x, s = 0..3) are added once, after the last tile.  A wave
+// runs its two panels' item lists in lockstep and reads the next step's
+// values and offsets together with the current step's B rows.  Items are
+// padded to four slots with value 0 on the zero row.
+//
+// Numerics.  Rows a slot's pattern lacks are multiplied by 0 here, as the
+// format's own padding slots are in the reference's kernels: with finite B
+// the sums equal the pattern bodies' to rounding, while an Inf or NaN in a B
+// row can reach a row of C that has no entry in that column (0 * Inf = NaN).
 //
 // Split K.  With more than one K range per (band, chunk), every unit writes
 // its partial tile to the workspace (write-through stores) and bumps the
@@ -45,8 +61,8 @@ constexpr int kBandWaves = 16;                // waves per unit, two panels each
 constexpr int kBandRows = 4 * kBandPanels;    // rows of C per band
 constexpr int kBandCols = 64;                 // columns of B and C per N chunk
 constexpr int kBandRowBytes = 4 * kBandCols;  // bytes of one staged B row
-constexpr int kBandImgHeader = 16;            // dwords of a wave image header
-constexpr int kBandImgMaxDw = 512;            // most dwords of one wave image
+constexpr int kBandImgHeader = 4;             // dwords of a wave image header
+constexpr int kBandImgMaxDw = 768;            // most dwords of one wave image (3 x 16 bytes a lane)
 constexpr size_t kBandLdsBytes = 160 * 1024;
 // The workspace of a plan with a band layout: partial tiles of at most
 // kBandTargetUnits units (every geometry keeps units * chunks * bands under
@@ -57,28 +73,21 @@ constexpr size_t kBandCounters = kBandTargetUnits;
 static_assert(kBandWorkFloats == kSplitWorkFloats && kBandCounters <= kSplitCounters,
               "the band kernel's split K fits the plan workspace");
 
-// Wave image (dwords), one per (band, K tile, wave), 16-byte aligned:
-//   [0], [1]  dense items of panels 0 and 1 (nd0, nd1)
-//   [2]       single items (a multiple of 4)
-//   [3], [4]  dword offsets of the dense and the single item areas
-//   [5]       max(nd0, nd1)
-//   [6..15]   0
-// Dense area: item 0 is a zero item (the zero row, values 0), then panel 0's
-// items, then panel 1's; a wave runs the two panels' lists in lockstep and
-// the shorter list reads the zero item.  Single area: the single items of the
-// eight lists k = 4p + r (panel p, row r) one list after another, padded to a
-// multiple of four items with zero items of list 0.
-//   dense item (20 dwords): the byte offsets of its four slots' rows in the
-//     staged B tile (row * 256), then its 16 values laid out [panel row i]
-//     [slot k], so that lane l reads its row's four values (l % 4) at once;
-//   single item (8 dwords): the byte offsets of its four entries' rows, the
-//     first one with the item's list k in its low bits (offsets are
-//     multiples of 256), then the four values.
-constexpr int kBandDenseDw = 20;
-constexpr int kBandSingleDw = 8;
+// Wave image (dwords), one per (band, wave, K tile) and stored in that
+// order (a wave's tiles one after another), 16-byte aligned:
+//   [0], [1]  items of panels 0 and 1 (n0, n1)
+//   [2]       max(n0, n1)
+//   [3]       0
+// then the items: item 0 is the zero item (the zero row, values 0), then
+// panel 0's n0 items, then panel 1's n1.  A wave runs the two panels' lists in
+// lockstep and the shorter list reads the zero item.
+//   item (20 dwords): its 16 values laid out [slot k][panel row i] (0 where
+//     slot k's pattern lacks row i), then the byte offsets of its four slots'
+//     rows in the staged B tile (row * 256; the zero row for padding slots).
+constexpr int kBandItemDw = 20;
 struct BandView {
   const int *img;   // wave images, 16-byte aligned each
-  const int *woff;  // first dword of image (band * ntiles + tile) * 16 + wave, + end
+  const int *woff;  // first dword of image (band * 16 + wave) * ntiles + tile, + end
   int nbands;
   int ntiles;
   int KT;           // B rows per K tile
@@ -97,15 +106,18 @@ struct BandGeometry {
   int counters = 0;
 };
 
-inline size_t band_stage_bytes(int KT) { return (size_t)(KT + 1) * kBandRowBytes; }
+__host__ __device__ inline size_t band_stage_bytes(int KT) { return (size_t)(KT + 1) * kBandRowBytes; }
 
-// The epilogue reuses the LDS for the single items' partial sums: 8 KiB per
-// wave ([panel][row][slot group][64 columns]) and one flag.
-constexpr size_t kBandRedBytes = (size_t)kBandWaves * 2 * 4 * 4 * kBandCols * sizeof(float) + 16;
+// After the last tile the LDS holds each wave's sums, one column per lane:
+// 2 KiB a wave ([panel][row][64 columns]); the split-K flag follows both.
+constexpr size_t kBandRedBytes = (size_t)kBandWaves * 2 * 4 * kBandCols * sizeof(float);
 
-inline size_t band_lds_bytes(int KT, int wimg_dw) {
-  return std::max(2 * band_stage_bytes(KT) + (size_t)kBandWaves * wimg_dw * 4, kBandRedBytes);
+__host__ __device__ inline size_t band_flag_offset(int KT, int wimg_dw) {
+  const size_t a = 2 * band_stage_bytes(KT) + (size_t)kBandWaves * wimg_dw * 4;
+  return a > kBandRedBytes ? a : kBandRedBytes;
 }
+
+inline size_t band_lds_bytes(int KT, int wimg_dw) { return band_flag_offset(KT, wimg_dw) + 16; }
 
 // units: the most units the grid may hold (kBandTargetUnits for the plan's
 // own workspace); work_cap: floats of workspace available.
@@ -122,6 +134,7 @@ inline BandGeometry band_geometry(const BandView &b, int N, int units = kBandTar
   while (nks > 1 && (size_t)nks * bc * kBandRows * kBandCols > work_cap) --nks;
   g.tpu = (b.ntiles + nks - 1) / nks;
   g.nks = (b.ntiles + g.tpu - 1) / g.tpu;
+  if (g.tpu + 1 > 64) return g;  // a unit's image offsets sit in one register, a lane per tile
   g.grid = (unsigned)(bc * g.nks);
   g.work_floats = g.nks > 1 ? (size_t)g.nks * bc * kBandRows * kBandCols : 0;
   g.counters = g.nks > 1 ? (int)bc : 0;
@@ -135,75 +148,24 @@ typedef int vec2i __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) vec2i lds_int2;
 typedef __attribute__((address_space(3))) char lds_char;
 
-// The dense items of one lockstep step: item ja of panel 0 and jb of panel
-// 1 (item 0 is the zero item), 16 MFMA blocks per slot.  tileb: this
-// lane's column in the staged B tile (lane l -> column l).
-__device__ __forceinline__ void band_dense_step(const lds_int *dense, int ja, int jb, const lds_char *tileb, int lane,
-                                                vec4f_t (&D)[2][2]) {
-  const vec4i ca = *(const lds_int4 *)(dense + kBandDenseDw * ja);
-  const vec4i cb = *(const lds_int4 *)(dense + kBandDenseDw * jb);
-  const vec4f a = *(const lds_float4 *)(dense + kBandDenseDw * ja + 4 + 4 * (lane & 3));
-  const vec4f b = *(const lds_float4 *)(dense + kBandDenseDw * jb + 4 + 4 * (lane & 3));
-  const float a0 = *(const lds_float *)(tileb + ca.x);
-  const float a1 = *(const lds_float *)(tileb + ca.y);
-  const float a2 = *(const lds_float *)(tileb + ca.z);
-  const float a3 = *(const lds_float *)(tileb + ca.w);
-  const float b0 = *(const lds_float *)(tileb + cb.x);
-  const float b1 = *(const lds_float *)(tileb + cb.y);
-  const float b2 = *(const lds_float *)(tileb + cb.z);
-  const float b3 = *(const lds_float *)(tileb + cb.w);
-  D[0][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a.x, a0, D[0][0], 0, 0, 0);
-  D[1][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(b.x, b0, D[1][0], 0, 0, 0);
-  D[0][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a.y, a1, D[0][1], 0, 0, 0);
-  D[1][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(b.y, b1, D[1][1], 0, 0, 0);
-  D[0][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a.z, a2, D[0][0], 0, 0, 0);
-  D[1][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(b.z, b2, D[1][0], 0, 0, 0);
-  D[0][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a.w, a3, D[0][1], 0, 0, 0);
-  D[1][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(b.w, b3, D[1][1], 0, 0, 0);
-}
+// One lockstep step: item ja of panel 0 and jb of panel 1 (item 0 is the
+// zero item), this lane's A value and B-row offset of each.  aoff: byte
+// offset of the lane's value in an item (slot s = lane / 16, row lane % 4);
+// ooff: byte offset of slot s's B-row offset.
+struct BandStep {
+  float a, b;
+  int oa, ob;
+};
 
-// acc[0..3] += v * x[0..3] as four v_fmac_f32.  Volatile asm: the eight
-// lists' cases of a switch stay apart, so the compiler cannot merge them into
-// one update through a dynamic (scratch memory) index of the accumulators.
-#define SC_BAND_FMA4(a, v, x)                                                                          \
-  asm volatile("v_fmac_f32 %0, %4, %5\n\tv_fmac_f32 %1, %4, %6\n\tv_fmac_f32 %2, %4, %7\n\tv_fmac_f32 %3, %4, %8" \
-               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3])                                         \
-               : "v"(v), "v"(x.x), "v"(x.y), "v"(x.z), "v"(x.w))
-
-__device__ __forceinline__ void band_single_acc(int k, float v, const vec4f &x, float (&acc)[2][4][4]) {
-  switch (k) {  // uniform: scalar branches
-    case 0: SC_BAND_FMA4(acc[0][0], v, x); break;
-    case 1: SC_BAND_FMA4(acc[0][1], v, x); break;
-    case 2: SC_BAND_FMA4(acc[0][2], v, x); break;
-    case 3: SC_BAND_FMA4(acc[0][3], v, x); break;
-    case 4: SC_BAND_FMA4(acc[1][0], v, x); break;
-    case 5: SC_BAND_FMA4(acc[1][1], v, x); break;
-    case 6: SC_BAND_FMA4(acc[1][2], v, x); break;
-    default: SC_BAND_FMA4(acc[1][3], v, x); break;
-  }
-}
-
-// Four single items from item j on: lane (s, g) takes entry s = lane / 16 of
-// each and columns 4g .. 4g+3.  All loads first, then the updates.  tileg:
-// column group g in the staged B tile.
-__device__ __forceinline__ void band_single_group(const lds_int *single, int j, int s, const lds_char *tileg,
-                                                  float (&acc)[2][4][4]) {
-  int o[4];
-  float v[4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    o[u] = single[kBandSingleDw * (j + u) + s];
-    v[u] = *(const lds_float *)(single + kBandSingleDw * (j + u) + 4 + s);
-  }
-  int k[4];
-  vec4f x[4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    k[u] = uniform(o[u]) & 7;  // lane 0 holds entry 0, whose low bits carry the list
-    x[u] = *(const lds_float4 *)(tileg + (o[u] & ~255));
-  }
-#pragma unroll
-  for (int u = 0; u < 4; ++u) band_single_acc(k[u], v[u], x[u], acc);
+__device__ __forceinline__ BandStep band_load_step(const lds_char *items, int ja, int jb, int aoff, int ooff) {
+  BandStep s;
+  const lds_char *ia = items + kBandItemDw * 4 * ja;
+  const lds_char *ib = items + kBandItemDw * 4 * jb;
+  s.a = *(const lds_float *)(ia + aoff);
+  s.b = *(const lds_float *)(ib + aoff);
+  s.oa = *(const lds_int *)(ia + ooff);
+  s.ob = *(const lds_int *)(ib + ooff);
+  return s;
 }
 
 // The band kernel (km = 4).  blockDim.x = 64 * kBandWaves.  Unit u of the
@@ -214,6 +176,7 @@ __global__ void __launch_bounds__(64 * kBandWaves)
                 int N, int nbands, int ntiles, int KT, int wimg_dw, int nch, int nks, int tpu, int accumulate) {
   extern __shared__ float4 smem4[];
   constexpr int Q4 = kBandCols / 4;  // float4 per staged B row
+  constexpr int IQ = kBandImgMaxDw / 256;  // float4 of a wave image per lane
   const int u = blockIdx.x;
   const int chunk = u % nch;
   const int ks = (u / nch) % nks;
@@ -248,36 +211,40 @@ __global__ void __launch_bounds__(64 * kBandWaves)
                                        0);
     }
   };
-  // the wave's image of tile t: at most 2 float4 per lane, in registers until
-  // the wave is done with the previous image
-  vec4i prei[2];
+  // the offsets of this wave's images of tiles t0 .. t1 (and the end of the
+  // last), lane t - t0 holding tile t's: read once, so that no tile waits
+  // for a scalar load of its image's place
+  const int *wo = woff + (size_t)(band * kBandWaves + w) * ntiles + t0;
+  const int woffv = lane <= t1 - t0 ? wo[lane] : 0;
+  // the wave's image of tile t: at most IQ float4 per lane, in registers
+  // until the wave is done with the previous image; its header goes to
+  // scalar registers when it is put to LDS
+  vec4i prei[IQ];
   int nimg = 0;
+  vec4i hdr = vec4i{0, 0, 0, 0};
   auto fetch_img = [&](int t) {
-    const int a0 = woff[(band * ntiles + t) * kBandWaves + w];
-    nimg = woff[(band * ntiles + t) * kBandWaves + w + 1] - a0;  // dwords, a multiple of 4
+    const int a0 = __builtin_amdgcn_readlane(woffv, t - t0);
+    nimg = __builtin_amdgcn_readlane(woffv, t - t0 + 1) - a0;  // dwords, a multiple of 4
     const vec4i *src = reinterpret_cast<const vec4i *>(img + a0);
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
+    for (int q = 0; q < IQ; ++q)
       if (4 * (lane + 64 * q) < nimg) prei[q] = __builtin_nontemporal_load(src + lane + 64 * q);
   };
   auto put_img = [&]() {
     lds_int4 *dst = (lds_int4 *)wimg;
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
+    for (int q = 0; q < IQ; ++q)
       if (4 * (lane + 64 * q) < nimg) dst[lane + 64 * q] = prei[q];
+    hdr = uniform4(prei[0]);  // lane 0: the image's first four dwords
   };
 
-  vec4f_t D[2][2];
-  float acc[2][4][4];
+  // D[p][q]: panel p, column 4x + q of slot s's partial sum in lane
+  // 16s + x (x = lane % 16), register i row i of the panel
+  vec4f_t D[2][4];
 #pragma unroll
-  for (int p = 0; p < 2; ++p) {
+  for (int p = 0; p < 2; ++p)
 #pragma unroll
-    for (int i = 0; i < 2; ++i) D[p][i] = vec4f_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) acc[p][r][e] = 0.f;
-  }
+    for (int q = 0; q < 4; ++q) D[p][q] = vec4f_t{0.f, 0.f, 0.f, 0.f};
 
   if (t0 < t1) {
     dma(0, t0);
@@ -286,6 +253,8 @@ __global__ void __launch_bounds__(64 * kBandWaves)
   }
   __builtin_amdgcn_s_waitcnt(0);  // the DMA of the first tile has landed
   __syncthreads();
+  const int aoff = 4 * (4 * (lane >> 4) + (lane & 3));
+  const int ooff = 64 + 4 * (lane >> 4);
   for (int t = t0; t < t1; ++t) {
     const int st = (t - t0) & 1;
     const bool more = t + 1 < t1;
@@ -294,51 +263,72 @@ __global__ void __launch_bounds__(64 * kBandWaves)
       fetch_img(t + 1);
     }
     {
-      // the wave image header, as scalars
-      const lds_int4 *h4 = (const lds_int4 *)wimg;
-      const vec4i h0 = uniform4(h4[0]), h1 = uniform4(h4[1]);
-      const lds_int *dense = wimg + h0.w;
-      const lds_int *single = wimg + h1.x;
-      // the stage; the byte offsets in the image add to it
-      const lds_char *tbase = (const lds_char *)lds + (size_t)st * stage_bytes;
-      const lds_char *tileb = tbase + 4 * lane;
-      const lds_char *tileg = tbase + 16 * (lane & 15);
-      // dense items: the two panels' lists in lockstep
-      const int nd0 = h0.x, nd1 = h0.y;
-      for (int i = 0; i < h1.y; ++i)
-        band_dense_step(dense, i < nd0 ? 1 + i : 0, i < nd1 ? 1 + nd0 + i : 0, tileb, lane, D);
-      // single items: four at a time
-      const int s = lane >> 4;
-      for (int j = 0; j < h0.z; j += 4) band_single_group(single, j, s, tileg, acc);
+      const vec4i h = hdr;
+      const lds_char *items = (const lds_char *)(wimg + kBandImgHeader);
+      // this lane's 16 bytes (columns 4x .. 4x+3) of a staged row; the byte
+      // offsets in the items add to it
+      const lds_char *tileb = (const lds_char *)lds + (size_t)st * stage_bytes + 16 * (lane & 15);
+      const int na = h.x, nb = h.y, nmax = h.z;
+      BandStep cur = band_load_step(items, na > 0 ? 1 : 0, nb > 0 ? 1 + na : 0, aoff, ooff);
+      for (int i = 0; i < nmax; ++i) {
+        // the next step's values and offsets first (past the lists' ends:
+        // the zero item), then this step's B rows: LDS reads return in
+        // order, so the one wait for the B rows also covers the next step,
+        // and both round trips overlap
+        const lds_char *pa = tileb + cur.oa, *pb = tileb + cur.ob;
+        __builtin_amdgcn_sched_barrier(0);
+        const int j = i + 1;
+        const BandStep nxt = band_load_step(items, j < na ? 1 + j : 0, j < nb ? 1 + na + j : 0, aoff, ooff);
+        __builtin_amdgcn_sched_barrier(0);
+        const vec4f xa = *(const lds_float4 *)pa;
+        const vec4f xb = *(const lds_float4 *)pb;
+        __builtin_amdgcn_sched_barrier(0);
+        D[0][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(cur.a, xa.x, D[0][0], 0, 0, 0);
+        D[1][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(cur.b, xb.x, D[1][0], 0, 0, 0);
+        D[0][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(cur.a, xa.y, D[0][1], 0, 0, 0);
+        D[1][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(cur.b, xb.y, D[1][1], 0, 0, 0);
+        D[0][2] = __builtin_amdgcn_mfma_f32_4x4x1f32(cur.a, xa.z, D[0][2], 0, 0, 0);
+        D[1][2] = __builtin_amdgcn_mfma_f32_4x4x1f32(cur.b, xb.z, D[1][2], 0, 0, 0);
+        D[0][3] = __builtin_amdgcn_mfma_f32_4x4x1f32(cur.a, xa.w, D[0][3], 0, 0, 0);
+        D[1][3] = __builtin_amdgcn_mfma_f32_4x4x1f32(cur.b, xb.w, D[1][3], 0, 0, 0);
+        cur = nxt;
+      }
     }
     if (more) put_img();  // the wave is done with its previous image
     __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA of the next tile has landed
     __syncthreads();
   }
 
-  // single-item sums: every slot group s writes its partial row sums (4
-  // columns per lane) to LDS, then lane l adds the four groups' values of
-  // column l to its MFMA tiles.  The stages are free after the loop's last
-  // barrier; each wave uses its own 8 KiB.
-  const int s = lane >> 4;
-  const int g = lane & 15;
-  lds_float *red = (lds_float *)lds + w * (2 * 4 * 4 * kBandCols);  // [p][r][s][64]
+  // the four slots' partial sums: lanes x, 16 + x, 32 + x, 48 + x into lane x
 #pragma unroll
   for (int p = 0; p < 2; ++p)
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      *(lds_float4 *)(red + ((p * 4 + r) * 4 + s) * kBandCols + 4 * g) =
-          vec4f{acc[p][r][0], acc[p][r][1], acc[p][r][2], acc[p][r][3]};
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = D[p][q][i];
+        v += lane_down<32>(v);
+        v += lane_down<16>(v);
+        D[p][q][i] = v;
+      }
+  // to one column per lane through LDS (the stages are free after the
+  // loop's last barrier; each wave its own 2 KiB, [p][row][64 columns])
+  lds_float *red = (lds_float *)lds + w * (2 * 4 * kBandCols);
+  if (lane < 16) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *(lds_float4 *)(red + (p * 4 + i) * kBandCols + 4 * lane) =
+            vec4f{D[p][0][i], D[p][1][i], D[p][2][i], D[p][3][i]};
+  }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes are done
   __builtin_amdgcn_wave_barrier();
   float out[2][4];
 #pragma unroll
   for (int p = 0; p < 2; ++p)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const lds_float *q = red + (p * 4 + i) * 4 * kBandCols + lane;
-      out[p][i] = D[p][0][i] + D[p][1][i] + ((q[0] + q[kBandCols]) + (q[2 * kBandCols] + q[3 * kBandCols]));
-    }
+    for (int i = 0; i < 4; ++i) out[p][i] = red[(p * 4 + i) * kBandCols + lane];
 
   // rows of this wave: band * 128 + (2w + p) * 4 + i, column n0 + lane
   const int rbase = band * kBandRows + 8 * w;
@@ -367,7 +357,7 @@ __global__ void __launch_bounds__(64 * kBandWaves)
                          __HIP_MEMORY_SCOPE_AGENT);
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
   __syncthreads();
-  int *flag = (int *)lds + kBandWaves * 2 * 4 * 4 * kBandCols;  // past the reduction area
+  int *flag = (int *)(lds + band_flag_offset(KT, wimg_dw));
   unsigned *cnt = counters + bc;
   if (threadIdx.x == 0) {
     const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -605,12 +605,11 @@ sc_plan *build_plan(const sc::Cfmtx &cf, int32_t flags, const std::vector<PatInf
 }
 
 // ---- band layout (SC_PLAN_BANDS, kernel_m 4) -----------------------------
-// A panel's stored entries, split for the band kernel: the slots of the
-// all-ones pattern (four values each), and every other slot's entries by
-// panel row.  Each list in ascending column order.
+// A panel's slots for the band kernel, every pattern together in ascending
+// column order, each with its four row values (0 for the rows its pattern
+// lacks).
 struct BandPanel {
-  std::vector<std::pair<int32_t, std::array<float, 4>>> dense;
-  std::vector<std::pair<int32_t, float>> rows[4];
+  std::vector<std::pair<int32_t, std::array<float, 4>>> slots;
 };
 
 struct BandHost {
@@ -634,19 +633,14 @@ std::vector<BandPanel> band_panels(const sc::Cfmtx &cf, const std::vector<PatInf
       BandPanel &bp = out[(size_t)q];
       for (int32_t j = a; j < e; ++j) {
         const float *v = &p.val32[(size_t)j * pop];
-        if (info[i].mask == 0xFu) {
-          bp.dense.push_back({p.cb[(size_t)j], {v[0], v[1], v[2], v[3]}});
-        } else {
-          for (int k = 0; k < nr; ++k) bp.rows[rows[k]].push_back({p.cb[(size_t)j], v[k]});
-        }
+        std::array<float, 4> x = {0.f, 0.f, 0.f, 0.f};
+        for (int k = 0; k < nr; ++k) x[(size_t)rows[k]] = v[k];
+        bp.slots.push_back({p.cb[(size_t)j], x});
       }
     }
   }
   auto by_col = [](const auto &x, const auto &y) { return x.first < y.first; };
-  for (BandPanel &bp : out) {
-    std::stable_sort(bp.dense.begin(), bp.dense.end(), by_col);
-    for (auto &r : bp.rows) std::stable_sort(r.begin(), r.end(), by_col);
-  }
+  for (BandPanel &bp : out) std::stable_sort(bp.slots.begin(), bp.slots.end(), by_col);
   return out;
 }
 
@@ -659,69 +653,44 @@ bool band_images(const std::vector<BandPanel> &panels, int32_t K, int KT, BandHo
   h.ntiles = (K + KT - 1) / KT;
   h.nbands = (npanels + sc::kBandPanels - 1) / sc::kBandPanels;
   const int32_t zero_off = KT * sc::kBandRowBytes;  // byte offset of the zero row
-  // cursors into each panel's lists: tiles are visited in order per panel
-  std::vector<size_t> dcur((size_t)npanels, 0), rcur((size_t)npanels * 4, 0);
+  // a cursor into each panel's slots: tiles are visited in order per panel
+  std::vector<size_t> cur((size_t)npanels, 0);
   h.woff.reserve((size_t)h.nbands * h.ntiles * sc::kBandWaves + 1);
   int max_dw = 0;
   struct Item {
-    int32_t off[4];
     float v[16];
+    int32_t off[4];
   };
-  const Item zero = {{zero_off, zero_off, zero_off, zero_off}, {0.f}};
-  std::vector<Item> dit, sit;
+  static_assert(sizeof(Item) == sc::kBandItemDw * 4, "item layout");
+  const Item zero = {{0.f}, {zero_off, zero_off, zero_off, zero_off}};
+  std::vector<Item> items;
   for (int b = 0; b < h.nbands; ++b)
-    for (int t = 0; t < h.ntiles; ++t) {
-      const int32_t klo = t * KT, khi = (int32_t)std::min<int64_t>((int64_t)K, (int64_t)klo + KT);
-      for (int w = 0; w < sc::kBandWaves; ++w) {
+    for (int w = 0; w < sc::kBandWaves; ++w)
+      for (int t = 0; t < h.ntiles; ++t) {
+        const int32_t klo = t * KT, khi = (int32_t)std::min<int64_t>((int64_t)K, (int64_t)klo + KT);
         int32_t hdr[sc::kBandImgHeader] = {0};
-        dit.assign(1, zero);
-        sit.clear();
+        items.assign(1, zero);
         for (int pp = 0; pp < 2; ++pp) {
           const int32_t q = b * sc::kBandPanels + 2 * w + pp;
           if (q >= npanels) continue;
           const BandPanel &bp = panels[(size_t)q];
-          // dense slots of the tile, four per item ([row][slot] values)
-          size_t &dc = dcur[(size_t)q];
-          const size_t d0 = dc;
-          while (dc < bp.dense.size() && bp.dense[dc].first < khi) ++dc;
-          for (size_t j = d0; j < dc; j += 4) {
+          // the panel's slots in the tile, four per item ([slot][row] values)
+          size_t &c = cur[(size_t)q];
+          const size_t c0 = c;
+          while (c < bp.slots.size() && bp.slots[c].first < khi) ++c;
+          for (size_t j = c0; j < c; j += 4) {
             Item it = zero;
-            for (int k = 0; k < 4 && j + k < dc; ++k) {
-              if (bp.dense[j + k].first < klo) throw sc::Error{SC_ERR_INTERNAL, "band layout lost a slot"};
-              it.off[k] = (bp.dense[j + k].first - klo) * sc::kBandRowBytes;
-              for (int i = 0; i < 4; ++i) it.v[4 * i + k] = bp.dense[j + k].second[(size_t)i];
+            for (int k = 0; k < 4 && j + k < c; ++k) {
+              if (bp.slots[j + k].first < klo) throw sc::Error{SC_ERR_INTERNAL, "band layout lost a slot"};
+              it.off[k] = (bp.slots[j + k].first - klo) * sc::kBandRowBytes;
+              for (int i = 0; i < 4; ++i) it.v[4 * k + i] = bp.slots[j + k].second[(size_t)i];
             }
-            dit.push_back(it);
+            items.push_back(it);
           }
-          hdr[pp] = (int32_t)((dc - d0 + 3) / 4);
-          // single entries of the tile, list k = 4 pp + r, four per item; the
-          // list rides in the low bits of the first offset
-          for (int r = 0; r < 4; ++r) {
-            const auto &lst = bp.rows[r];
-            size_t &rc = rcur[(size_t)q * 4 + r];
-            const size_t r0 = rc;
-            while (rc < lst.size() && lst[rc].first < khi) ++rc;
-            for (size_t j = r0; j < rc; j += 4) {
-              Item it = zero;
-              for (int k = 0; k < 4 && j + k < rc; ++k) {
-                if (lst[j + k].first < klo) throw sc::Error{SC_ERR_INTERNAL, "band layout lost an entry"};
-                it.off[k] = (lst[j + k].first - klo) * sc::kBandRowBytes;
-                it.v[k] = lst[j + k].second;
-              }
-              it.off[0] |= 4 * pp + r;
-              sit.push_back(it);
-            }
-          }
+          hdr[pp] = (int32_t)((c - c0 + 3) / 4);
         }
-        while (sit.size() % 4) sit.push_back(zero);
-        const int nd = (int)dit.size(), ns = (int)sit.size();
-        const int dense = sc::kBandImgHeader;
-        const int single = dense + sc::kBandDenseDw * nd;
-        const int total = (single + sc::kBandSingleDw * ns + 3) / 4 * 4;
-        hdr[2] = ns;
-        hdr[3] = dense;
-        hdr[4] = single;
-        hdr[5] = std::max(hdr[0], hdr[1]);
+        hdr[2] = std::max(hdr[0], hdr[1]);
+        const int total = (sc::kBandImgHeader + sc::kBandItemDw * (int)items.size() + 3) / 4 * 4;
         if (total > sc::kBandImgMaxDw) return false;
         max_dw = std::max(max_dw, total);
         if ((int64_t)h.img.size() + total > INT32_MAX)
@@ -730,23 +699,11 @@ bool band_images(const std::vector<BandPanel> &panels, int32_t K, int KT, BandHo
         const size_t o = h.img.size();
         h.img.resize(o + (size_t)total, 0);
         std::memcpy(&h.img[o], hdr, sizeof hdr);
-        for (int j = 0; j < nd; ++j) {
-          std::memcpy(&h.img[o + dense + sc::kBandDenseDw * j], dit[j].off, 4 * sizeof(int32_t));
-          std::memcpy(&h.img[o + dense + sc::kBandDenseDw * j + 4], dit[j].v, 16 * sizeof(float));
-        }
-        for (int j = 0; j < ns; ++j) {
-          std::memcpy(&h.img[o + single + sc::kBandSingleDw * j], sit[j].off, 4 * sizeof(int32_t));
-          std::memcpy(&h.img[o + single + sc::kBandSingleDw * j + 4], sit[j].v, 4 * sizeof(float));
-        }
+        std::memcpy(&h.img[o + sc::kBandImgHeader], items.data(), items.size() * sizeof(Item));
       }
-    }
   h.woff.push_back((int32_t)h.img.size());
-  for (int32_t q = 0; q < npanels; ++q) {
-    if (dcur[(size_t)q] != panels[(size_t)q].dense.size()) throw sc::Error{SC_ERR_INTERNAL, "band layout lost slots"};
-    for (int r = 0; r < 4; ++r)
-      if (rcur[(size_t)q * 4 + r] != panels[(size_t)q].rows[r].size())
-        throw sc::Error{SC_ERR_INTERNAL, "band layout lost entries"};
-  }
+  for (int32_t q = 0; q < npanels; ++q)
+    if (cur[(size_t)q] != panels[(size_t)q].slots.size()) throw sc::Error{SC_ERR_INTERNAL, "band layout lost slots"};
   h.wimg_dw = std::max(max_dw, 4);
   return true;
 }

@@ -1,7 +1,8 @@
 """GPU parity of the band kernel (SC_PLAN_BANDS, kernel_m 4, N a multiple of
-64): B staged in LDS per band of 128 rows and K tile, all-ones slots on the
-matrix cores, the other slots split into their rows, split K with the plan's
-workspace.  Against the CPU oracle on the same inputs.
+64): B staged in LDS per band of 128 rows and K tile, every slot on the
+matrix cores (four slots of one panel to an item, whatever their patterns),
+split K with the plan's workspace.  Against the CPU oracle on the same
+inputs.
 
 Floating point: max relative error <= 1e-5 normalised by (|A| |B|)_ij
 against the fp64 product of the same fp32 operands (with accumulate, by
