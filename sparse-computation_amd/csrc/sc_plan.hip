@@ -752,7 +752,7 @@ void build_band(sc_plan *plan, const sc::Cfmtx &cf, const std::vector<PatInfo> &
 int auto_waves(const sc_plan *p, int N) {
   if (p->npanels == 0) return 1;
   const sc::Geometry g1 = sc::geometry(p->km, N, 1, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes,
-                                   p->nslots / std::max(1, p->npanels));
+                                   p->nslots / std::max(1, p->npanels), p->npanels);
   const int S = 64 / g1.L;
   const double avg = (double)p->nslots / p->npanels;
   const double segs = (double)p->nsegs / p->npanels;
@@ -764,7 +764,7 @@ int auto_waves(const sc_plan *p, int N) {
   // against 7.2 with 7
   if ((N == 2 || N == 4) && sc::gather_lds_f32(N, 1, p->km, p->view.max_pslots, p->view.max_pvals)) w = std::min(w, 4);
   while (w > 1 && sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes,
-                                   p->nslots / std::max(1, p->npanels)).lds > 65536) --w;
+                                   p->nslots / std::max(1, p->npanels), p->npanels).lds > 65536) --w;
   return std::max(w, 1);
 }
 
@@ -828,7 +828,7 @@ int launch(const sc_plan *p, const sc_gen_record *rec, sc_gen_launch_fn fn, cons
     throw sc::Error{SC_ERR_ARG, "B and C must be aligned to their vector width (16 B when N % 4 == 0)"};
   int w = waves ? waves : (rec->waves ? rec->waves : auto_waves(p, N));
   if (sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes,
-                                   p->nslots / std::max(1, p->npanels)).lds > 65536)
+                                   p->nslots / std::max(1, p->npanels), p->npanels).lds > 65536)
     throw sc::Error{SC_ERR_ARG, "too many waves per panel for this N"};
   sc::DevView view = p->view;
   // the split-K workspace: the plan's, or the caller's scratch (nothing is
@@ -963,7 +963,7 @@ int sc_plan_describe(const sc_plan *p, int32_t N, char *buf, size_t buflen) {
     } else {
       const int w = auto_waves(p, N);
       const sc::Geometry g = sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes,
-                                   p->nslots / std::max(1, p->npanels));
+                                   p->nslots / std::max(1, p->npanels), p->npanels);
       if (sc::use_row_spmv(p->view, p->km, N, w)) {
         d = "row_spmv_kernel km=1 V=" + std::to_string(N) + " rows_per_workgroup=" + std::to_string(sc::kRowSpmvRows) + " grid=" +
             std::to_string((p->M + sc::kRowSpmvRows - 1) / sc::kRowSpmvRows);
@@ -973,7 +973,8 @@ int sc_plan_describe(const sc_plan *p, int32_t N, char *buf, size_t buflen) {
       } else {
         d = std::string(g.wide ? "wide_kernel" : "panel_kernel") + " km=" + std::to_string(p->km) + " V=" +
             std::to_string(g.V) + (g.wide ? "" : " L=" + std::to_string(g.L)) + " stage=" +
-            std::to_string(g.stage ? 1 : 0) + " waves=" + std::to_string(w) + " grid=" + std::to_string(p->npanels);
+            std::to_string(g.stage ? 1 : 0) + " waves=" + std::to_string(w) + " grid=" + std::to_string(p->npanels) +
+            (g.ny > 1 ? "x" + std::to_string(g.ny) : "");
       }
     }
     if (p->rows_of_km > 1) d += " (rows of km=" + std::to_string(p->rows_of_km) + ")";

@@ -14,7 +14,7 @@ import pytest
 
 import oracle as O
 import sc_amd
-from cases import REL_TOL, csr_f32, oracle_check, synth_case
+from cases import REL_TOL, csr_f32, oracle_check, oracle_check_acc, synth_case
 from conftest import FIXTURE_STEM
 
 torch = pytest.importorskip("torch")
@@ -63,6 +63,27 @@ def test_spmm_odd_and_wide_n(n):
     C = run_spmm(A, B, 4, 1)
     err, _ = oracle_check(A, B, C)
     assert err <= REL_TOL, (n, err)
+
+
+@pytest.mark.parametrize("n", [33, 100, 128])
+@pytest.mark.parametrize("waves", [0, 1, 5])
+def test_spmm_n_chunks_split_over_workgroups(n, waves):
+    # 128 long panels, fewer than the CUs: the lanes-over-slots kernel gives
+    # each panel two workgroups, one per half of the N chunk (grid 128 x 2)
+    A, B = synth_case(512, 2048, 0.30, n, seed=0x5EED0000 + 7300 + n)
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1), PAT)
+    d = plan.describe(n)
+    assert d.startswith("panel_kernel") and "grid=128x2" in d, d
+    Bt = torch.from_numpy(np.ascontiguousarray(B, np.float32)).to(DEV)
+    Ct = torch.full((512, n), float("nan"), device=DEV)
+    plan.spmm(Bt, Ct, waves=waves)
+    torch.cuda.synchronize()
+    assert oracle_check(A, B, Ct.cpu().numpy())[0] <= REL_TOL
+    C0 = np.random.default_rng(n).standard_normal((512, n)).astype(np.float32)
+    Ct = torch.from_numpy(C0.copy()).to(DEV)
+    plan.spmm(Bt, Ct, accumulate=True, waves=waves)
+    torch.cuda.synchronize()
+    assert oracle_check_acc(A, B, Ct.cpu().numpy(), C0) <= REL_TOL
 
 
 @pytest.mark.parametrize("waves", [1, 2, 3, 8, 16])
