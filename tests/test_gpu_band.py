@@ -112,6 +112,22 @@ def test_band_falls_back_off_its_shapes():
     assert err <= REL_TOL
 
 
+def test_band_falls_back_when_a_unit_would_hold_more_than_63_tiles():
+    # 64 bands x 4 chunks at N = 256 leave no room to split K, so a unit would
+    # hold all 79 K tiles, more than its image offsets' 64 lanes: the plan runs
+    # its other kernels; at N = 64 (4 K ranges of 20 tiles) it runs the band
+    # kernel
+    A, _ = synth_case(8192, 20000, 0.0005, 1, seed=0x5EED0000 + 7400)
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1), BANDS)
+    assert "tile_rows=256" in plan.describe(64), plan.describe(64)
+    assert not plan.describe(256).startswith("band_kernel"), plan.describe(256)
+    rng = np.random.default_rng(9)
+    for n in (64, 256):
+        B = rng.uniform(-1, 1, size=(20000, n)).astype(np.float32)
+        err, _ = oracle_check(A, B, run(plan, B))
+        assert err <= REL_TOL, (n, err)
+
+
 def test_band_empty_matrix_overwrites_c():
     A = sc_amd.Csr.from_arrays(300, 200, np.zeros(301, np.int32), [], [])
     plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1), BANDS)
