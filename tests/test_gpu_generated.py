@@ -45,27 +45,43 @@ def test_generated_unit_follows_the_layout_rule(n):
         assert oracle_check(A, B, C)[0] <= REL_TOL, (n, flags)
 
 
+# every unit on both layouts: its one-row body (default plans at these
+# sizes) and its km-row bodies (SC_PLAN_PATTERNS)
+LAYOUTS = [0, sc_amd.PLAN_PATTERNS]
+
+
+@pytest.mark.parametrize("flags", LAYOUTS)
 @pytest.mark.parametrize("n", [1, 32, 128])
-def test_generated_spmm_km4_kn2(n):
+def test_generated_spmm_km4_kn2(n, flags):
     A, B = synth_case(300, 256, 0.15, n, seed=41 + n)
     for kn in (2, 4, 8):  # packs of 2 divide all of these
-        C = run(sc_amd.Cfmtx.build(A, 4, kn), unit("spmm_km4_kn2"), B)
+        C = run(sc_amd.Cfmtx.build(A, 4, kn), unit("spmm_km4_kn2"), B, flags)
         assert oracle_check(A, B, C)[0] <= REL_TOL
 
 
-def test_generated_small_b_and_spmv():
+@pytest.mark.parametrize("flags", LAYOUTS)
+@pytest.mark.parametrize("n", [1, 7, 64])
+def test_generated_spmm_km3_kn1(n, flags):
+    A, B = synth_case(301, 190, 0.2, n, seed=47 + n)
+    C = run(sc_amd.Cfmtx.build(A, 3, 1), unit("spmm_km3_kn1"), B, flags)
+    assert oracle_check(A, B, C)[0] <= REL_TOL
+
+
+@pytest.mark.parametrize("flags", LAYOUTS)
+def test_generated_small_b_and_spmv(flags):
     A, B = synth_case(256, 200, 0.2, 2, seed=43)
-    C = run(sc_amd.Cfmtx.build(A, 4, 1), unit("spmm_small_km4_b2"), B)
+    C = run(sc_amd.Cfmtx.build(A, 4, 1), unit("spmm_small_km4_b2"), B, flags)
     assert oracle_check(A, B, C)[0] <= REL_TOL
     A, B = synth_case(256, 200, 0.2, 1, seed=44)
-    C = run(sc_amd.Cfmtx.build(A, 4, 3), unit("spmv_km4"), B)
+    C = run(sc_amd.Cfmtx.build(A, 4, 3), unit("spmv_km4"), B, flags)
     assert oracle_check(A, B, C)[0] <= REL_TOL
 
 
-def test_generated_dictionary_unit():
+@pytest.mark.parametrize("flags", LAYOUTS)
+def test_generated_dictionary_unit(flags):
     A, B = synth_case(96, 128, 0.3, 64, seed=45)
     cf = sc_amd.Cfmtx.build(A, 4, 1, os.path.join(GOLDEN, "dict4_sub.txt"))
-    C = run(cf, unit("spmm_km4_kn1", "spmm_km4_kn1_dict"), B)
+    C = run(cf, unit("spmm_km4_kn1", "spmm_km4_kn1_dict"), B, flags)
     # the format drops slots whose pattern is not in the dictionary: compare
     # with the product of what the format kept
     kept = sc_amd.Csr.from_arrays(96, 128, *_kept_csr(cf))
