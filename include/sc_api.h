@@ -124,12 +124,13 @@ void sc_cfmtx_free(sc_cfmtx *cf);
                                   one workgroup per row instead of per km rows  */
 #define SC_PLAN_PATTERNS 32    /* keep only the km-row pattern layout           */
 #define SC_PLAN_BANDS 64       /* kernel_m 4 files: also build the band layout (B
-                                  staged in LDS once per band of 128 rows and K
-                                  tile, all-ones slots on the matrix cores, split
-                                  K with a plan-owned workspace; the format's
-                                  zero padding slots are skipped); sc_spmm runs it
-                                  at N a multiple of 64 when the layout fits the
-                                  LDS                                            */
+                                  staged in LDS once per band of panels and K
+                                  range of up to 512 rows, every slot on the
+                                  matrix cores, split K over the ranges with a
+                                  plan-owned workspace; the format's zero
+                                  padding slots are skipped; K up to 8192);
+                                  sc_spmm runs it at N a multiple of 64 up to
+                                  256                                           */
 /* Without SC_PLAN_ROWS, SC_PLAN_PATTERNS, SC_PLAN_TILED or SC_PLAN_CHUNKED a
  * plan of a kernel_m > 1 file holds both layouts, and sc_spmm / sc_spmv run
  * the one-row layout while its B-row gathers (4 * stored entries * N bytes)
@@ -167,12 +168,13 @@ int sc_spmm(const sc_plan *plan, const float *dB, float *dC, int32_t N, int32_t 
  * forbid hipMalloc.  sc_spmm with the split-K kernels' partial sums and
  * arrival counters (SC_PLAN_BANDS, SC_PLAN_TILED) in the library's static
  * per-device scratch instead of the plan's workspace; allocates nothing.
- * The scratch is 8 MiB of partial sums plus 16 KiB of counters, held on each
- * GPU the library runs on until the process ends; the K split is sized to
- * fit it (as the plan's workspace, so results equal sc_spmm's), and a launch
- * that would need more is refused with SC_ERR_UNSUPPORTED.  Every call on one
- * GPU shares that GPU's scratch: calls that overlap on one GPU (other
- * streams, other threads) race. */
+ * The scratch is 16 MiB of partial sums plus 16 KiB of counters, held on each
+ * GPU the library runs on until the process ends; the launches are the ones
+ * sc_spmm makes on the same plan (so results equal sc_spmm's), and a launch
+ * whose partial sums or counters need more is refused with
+ * SC_ERR_UNSUPPORTED (the band kernel at N = 128 on a 4096-row plan with K =
+ * 4096 fits).  Every call on one GPU shares that GPU's scratch: calls that
+ * overlap on one GPU (other streams, other threads) race. */
 int sc_spmm_noalloc(const sc_plan *plan, const float *dB, float *dC, int32_t N, int32_t flags,
                     int32_t waves_per_panel, void *hip_stream);
 /* y = A*x (N = 1). */

@@ -101,6 +101,8 @@ struct sc_plan {
   void *band_mem = nullptr;
   float *band_work = nullptr;
   unsigned *band_cnt = nullptr;
+  size_t band_work_floats = 0;
+  size_t band_cnt_n = 0;
 };
 
 namespace {
@@ -614,7 +616,7 @@ struct BandPanel {
 
 struct BandHost {
   std::vector<int32_t> img, woff;
-  int nbands = 0, ntiles = 0, KT = 0, wimg_dw = 0;
+  int nbands = 0, nks = 0, KR = 0;
 };
 
 std::vector<BandPanel> band_panels(const sc::Cfmtx &cf, const std::vector<PatInfo> &info, bool drop_pad) {
@@ -644,87 +646,119 @@ std::vector<BandPanel> band_panels(const sc::Cfmtx &cf, const std::vector<PatInf
   return out;
 }
 
-// The wave images for K tiles of KT rows; false when one image would exceed
-// kBandImgMaxDw dwords.  Image layout: sc_band.hpp (BandView).
-bool band_images(const std::vector<BandPanel> &panels, int32_t K, int KT, BandHost &h) {
+// The wave records (layout: sc_band.hpp, BandView).  K ranges of up to
+// kBandMaxRange rows; bands of one to kBandWavePanels panels per wave, sized
+// so that bands x K ranges is about kBandTargetPairs; per (band, K range)
+// the panels go to the waves longest first, each onto the least loaded wave
+// that holds fewer than kBandWavePanels (load: its groups plus one per panel
+// for the hand-over), and a wave runs its panels in ascending order.
+void band_records(const std::vector<BandPanel> &panels, int32_t K, BandHost &h) {
   const int32_t npanels = (int32_t)panels.size();
   h = BandHost{};
-  h.KT = KT;
-  h.ntiles = (K + KT - 1) / KT;
-  h.nbands = (npanels + sc::kBandPanels - 1) / sc::kBandPanels;
-  const int32_t zero_off = KT * sc::kBandRowBytes;  // byte offset of the zero row
-  // a cursor into each panel's slots: tiles are visited in order per panel
+  h.KR = (int)std::min<int64_t>(sc::kBandMaxRange, ((int64_t)K + 3) / 4 * 4);
+  h.nks = (int)(((int64_t)K + h.KR - 1) / h.KR);
+  const int64_t want = ((int64_t)npanels * h.nks + sc::kBandTargetPairs - 1) / sc::kBandTargetPairs;
+  const int32_t P = (int32_t)std::min<int64_t>((int64_t)sc::kBandWaves * sc::kBandWavePanels,
+                                               std::max<int64_t>(sc::kBandWaves, want));
+  h.nbands = (npanels + P - 1) / P;
+  const int32_t zero_off = h.KR * sc::kBandRowBytes;  // byte offset of the zero row
+  // a cursor into each panel's slots: its K ranges are visited in order
   std::vector<size_t> cur((size_t)npanels, 0);
-  h.woff.reserve((size_t)h.nbands * h.ntiles * sc::kBandWaves + 1);
-  int max_dw = 0;
-  struct Item {
-    float v[16];
-    int32_t off[4];
-  };
-  static_assert(sizeof(Item) == sc::kBandItemDw * 4, "item layout");
-  const Item zero = {{0.f}, {zero_off, zero_off, zero_off, zero_off}};
-  std::vector<Item> items;
-  for (int b = 0; b < h.nbands; ++b)
-    for (int w = 0; w < sc::kBandWaves; ++w)
-      for (int t = 0; t < h.ntiles; ++t) {
-        const int32_t klo = t * KT, khi = (int32_t)std::min<int64_t>((int64_t)K, (int64_t)klo + KT);
-        int32_t hdr[sc::kBandImgHeader] = {0};
-        items.assign(1, zero);
-        for (int pp = 0; pp < 2; ++pp) {
-          const int32_t q = b * sc::kBandPanels + 2 * w + pp;
-          if (q >= npanels) continue;
-          const BandPanel &bp = panels[(size_t)q];
-          // the panel's slots in the tile, four per item ([slot][row] values)
-          size_t &c = cur[(size_t)q];
-          const size_t c0 = c;
-          while (c < bp.slots.size() && bp.slots[c].first < khi) ++c;
-          for (size_t j = c0; j < c; j += 4) {
-            Item it = zero;
-            for (int k = 0; k < 4 && j + k < c; ++k) {
-              if (bp.slots[j + k].first < klo) throw sc::Error{SC_ERR_INTERNAL, "band layout lost a slot"};
-              it.off[k] = (bp.slots[j + k].first - klo) * sc::kBandRowBytes;
-              for (int i = 0; i < 4; ++i) it.v[4 * k + i] = bp.slots[j + k].second[(size_t)i];
-            }
-            items.push_back(it);
-          }
-          hdr[pp] = (int32_t)((c - c0 + 3) / 4);
+  h.woff.reserve((size_t)h.nbands * h.nks * sc::kBandWaves + 1);
+  std::vector<int32_t> rec;
+  for (int b = 0; b < h.nbands; ++b) {
+    const int32_t q0 = b * P, q1 = std::min(npanels, q0 + P), nq = q1 - q0;
+    std::vector<size_t> c0((size_t)nq), c1((size_t)nq);
+    std::vector<int32_t> ngr((size_t)nq), order((size_t)nq);
+    for (int ks = 0; ks < h.nks; ++ks) {
+      const int32_t klo = ks * h.KR;
+      const int64_t khi = std::min<int64_t>((int64_t)K, (int64_t)klo + h.KR);
+      for (int32_t i = 0; i < nq; ++i) {
+        const BandPanel &bp = panels[(size_t)(q0 + i)];
+        size_t &c = cur[(size_t)(q0 + i)];
+        c0[(size_t)i] = c;
+        while (c < bp.slots.size() && bp.slots[c].first < khi) {
+          if (bp.slots[c].first < klo) throw sc::Error{SC_ERR_INTERNAL, "band layout lost a slot"};
+          ++c;
         }
-        hdr[2] = std::max(hdr[0], hdr[1]);
-        const int total = (sc::kBandImgHeader + sc::kBandItemDw * (int)items.size() + 3) / 4 * 4;
-        if (total > sc::kBandImgMaxDw) return false;
-        max_dw = std::max(max_dw, total);
-        if ((int64_t)h.img.size() + total > INT32_MAX)
+        c1[(size_t)i] = c;
+        const size_t items = (c - c0[(size_t)i] + 3) / 4;
+        ngr[(size_t)i] = (int32_t)std::max<size_t>(1, (items + 3) / 4);  // an empty panel: one group of zeros
+        order[(size_t)i] = i;
+      }
+      std::stable_sort(order.begin(), order.end(),
+                       [&](int32_t x, int32_t y) { return ngr[(size_t)x] > ngr[(size_t)y]; });
+      std::vector<std::vector<int32_t>> wp(sc::kBandWaves);
+      int64_t load[sc::kBandWaves] = {0};
+      for (int32_t i : order) {
+        int best = -1;
+        for (int w = 0; w < sc::kBandWaves; ++w)
+          if ((int)wp[(size_t)w].size() < sc::kBandWavePanels && (best < 0 || load[w] < load[best])) best = w;
+        wp[(size_t)best].push_back(i);
+        load[best] += ngr[(size_t)i] + 1;
+      }
+      for (int w = 0; w < sc::kBandWaves; ++w) {
+        std::vector<int32_t> &mine = wp[(size_t)w];
+        std::sort(mine.begin(), mine.end());
+        int32_t groups = 0;
+        for (int32_t i : mine) groups += ngr[(size_t)i];
+        const size_t ptab_dw = (2 * mine.size() + 3) / 4 * 4;
+        const size_t nblk = std::max<size_t>(1, ((size_t)groups + 3) / 4);
+        rec.assign((size_t)sc::kBandRecHeader + ptab_dw + nblk * sc::kBandBlockDw, 0);
+        rec[0] = (int32_t)mine.size();
+        rec[1] = groups;
+        rec[2] = (int32_t)nblk;
+        for (size_t k = 0; k < mine.size(); ++k) {
+          rec[sc::kBandRecHeader + 2 * k] = q0 + mine[k];
+          rec[sc::kBandRecHeader + 2 * k + 1] = ngr[(size_t)mine[k]];
+        }
+        // every offset starts on the zero row (padding items and groups)
+        const size_t base = sc::kBandRecHeader + ptab_dw;
+        for (size_t b = 0; b < nblk; ++b)
+          for (int l = 0; l < 64; ++l) rec[base + b * sc::kBandBlockDw + 256 + (size_t)l] = zero_off;
+        size_t gi = 0;  // the wave's group index
+        for (int32_t i : mine) {
+          const BandPanel &bp = panels[(size_t)(q0 + i)];
+          for (int32_t G = 0; G < ngr[(size_t)i]; ++G, ++gi) {
+            int32_t *bk = &rec[base + (gi / 4) * sc::kBandBlockDw];
+            const int g4 = (int)(gi % 4);
+            for (int t = 0; t < 4; ++t)
+              for (int s4 = 0; s4 < 4; ++s4) {
+                const size_t j = c0[(size_t)i] + 4 * (4 * (size_t)G + t) + s4;
+                if (j >= c1[(size_t)i]) continue;
+                bk[256 + 16 * s4 + 4 * g4 + t] = (bp.slots[j].first - klo) * sc::kBandRowBytes;
+                for (int r = 0; r < 4; ++r)
+                  std::memcpy(&bk[4 * (16 * s4 + 4 * t + r) + g4], &bp.slots[j].second[(size_t)r], 4);
+              }
+          }
+        }
+        if ((int64_t)h.img.size() + (int64_t)rec.size() > INT32_MAX)
           throw sc::Error{SC_ERR_UNSUPPORTED, "band layout larger than int32 offsets"};
         h.woff.push_back((int32_t)h.img.size());
-        const size_t o = h.img.size();
-        h.img.resize(o + (size_t)total, 0);
-        std::memcpy(&h.img[o], hdr, sizeof hdr);
-        std::memcpy(&h.img[o + sc::kBandImgHeader], items.data(), items.size() * sizeof(Item));
+        h.img.insert(h.img.end(), rec.begin(), rec.end());
+        h.img.resize((h.img.size() + 3) / 4 * 4, 0);  // 16-byte aligned records
       }
+    }
+  }
   h.woff.push_back((int32_t)h.img.size());
   for (int32_t q = 0; q < npanels; ++q)
     if (cur[(size_t)q] != panels[(size_t)q].slots.size()) throw sc::Error{SC_ERR_INTERNAL, "band layout lost slots"};
-  h.wimg_dw = std::max(max_dw, 4);
-  return true;
 }
 
-// Build and upload the band layout of a kernel_m 4 plan: the largest K tile
-// (256 rows down to 32) whose two B stages and sixteen wave images fit the
-// LDS.  A plan whose images fit no tile gets no band layout.
+// Build and upload the band layout of a kernel_m 4 plan, with the split-K
+// workspace (partial tiles for N up to 64 * kBandMaxChunks) and arrival
+// counters it needs, so that no launch allocates.
 void build_band(sc_plan *plan, const sc::Cfmtx &cf, const std::vector<PatInfo> &info) {
   if (cf.km != 4) throw sc::Error{SC_ERR_UNSUPPORTED, "the band layout needs kernel_m 4"};
   if (cf.n <= 0 || cf.npanels() <= 0) return;
   // the format's zero padding slots (kernel_n packs) are never computed here:
   // they repeat their segment's last column with value 0
   const std::vector<BandPanel> panels = band_panels(cf, info, true);
+  // more K ranges than this and the partial sums outweigh the staging saved
+  if (((int64_t)cf.n + sc::kBandMaxRange - 1) / sc::kBandMaxRange > sc::kBandMaxRanges) return;
   BandHost h;
-  bool ok = false;
-  for (int KT = 256; KT >= 32 && !ok; KT -= 32) {
-    if (!band_images(panels, cf.n, KT, h)) continue;
-    const size_t lds = sc::band_lds_bytes(KT, h.wimg_dw);
-    ok = lds <= sc::kBandLdsBytes;
-  }
-  if (!ok) return;  // the plan runs its other kernels
+  band_records(panels, cf.n, h);
+  if (sc::band_lds_bytes(h.KR) > sc::kBandLdsBytes) return;  // the plan runs its other kernels
   const size_t off_woff = align_up<int>(h.img.size() * sizeof(int32_t));
   const size_t total = align_up<int>(off_woff + h.woff.size() * sizeof(int32_t));
   hip_check(hipMalloc(&plan->band_mem, total), "hipMalloc(band layout)");
@@ -732,16 +766,21 @@ void build_band(sc_plan *plan, const sc::Cfmtx &cf, const std::vector<PatInfo> &
   std::memcpy(host.data(), h.img.data(), h.img.size() * sizeof(int32_t));
   std::memcpy(host.data() + off_woff, h.woff.data(), h.woff.size() * sizeof(int32_t));
   hip_check(hipMemcpy(plan->band_mem, host.data(), total, hipMemcpyHostToDevice), "hipMemcpy(band layout)");
-  hip_check(hipMalloc((void **)&plan->band_work, sc::kBandWorkFloats * sizeof(float)), "hipMalloc(band workspace)");
-  hip_check(hipMalloc((void **)&plan->band_cnt, sc::kBandCounters * sizeof(unsigned)), "hipMalloc(band counters)");
-  hip_check(hipMemset(plan->band_cnt, 0, sc::kBandCounters * sizeof(unsigned)), "hipMemset(band counters)");
+  plan->band_work_floats = sc::band_partial_floats(h.nks, cf.npanels(), sc::kBandMaxChunks);
+  plan->band_cnt_n = h.nks > 1 ? (size_t)cf.npanels() * sc::kBandMaxChunks : 0;
+  if (plan->band_work_floats) {
+    hip_check(hipMalloc((void **)&plan->band_work, plan->band_work_floats * sizeof(float)),
+              "hipMalloc(band workspace)");
+    hip_check(hipMalloc((void **)&plan->band_cnt, plan->band_cnt_n * sizeof(unsigned)), "hipMalloc(band counters)");
+    hip_check(hipMemset(plan->band_cnt, 0, plan->band_cnt_n * sizeof(unsigned)), "hipMemset(band counters)");
+  }
   hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize(band layout)");
   plan->band.img = (const int *)plan->band_mem;
   plan->band.woff = (const int *)((unsigned char *)plan->band_mem + off_woff);
   plan->band.nbands = h.nbands;
-  plan->band.ntiles = h.ntiles;
-  plan->band.KT = h.KT;
-  plan->band.wimg_dw = h.wimg_dw;
+  plan->band.nks = h.nks;
+  plan->band.KR = h.KR;
+  plan->band.npanels = cf.npanels();
 }
 
 // Waves per panel: enough waves in the grid to cover the 256 CUs several
@@ -846,20 +885,22 @@ int launch(const sc_plan *p, const sc_gen_record *rec, sc_gen_launch_fn fn, cons
   return SC_OK;
 }
 
-// The band kernel when the plan has a band layout and N fits it; false
-// otherwise.  work / counters: the split-K workspace to use (work_cap floats).
+// The band kernel when the plan has a band layout and N fits it and the
+// given workspace; false otherwise.  work / counters: the split-K workspace
+// to use (work_cap floats, counter_cap counters); clear: zero the counters
+// first (a caller's scratch).
 bool launch_band(const sc_plan *p, const float *B, float *C, int32_t N, int32_t flags, void *stream, float *work,
-                 unsigned *counters, size_t work_cap, bool clear = false) {
+                 unsigned *counters, size_t work_cap, size_t counter_cap, bool clear = false) {
   if (!p->band.img) return false;
-  const sc::BandGeometry g = sc::band_geometry(p->band, N, sc::kBandTargetUnits, work_cap);
+  const sc::BandGeometry g = sc::band_geometry(p->band, N, work_cap, counter_cap);
   if (!g.use) return false;
-  if (clear && g.nks > 1) clear_counters(counters, (size_t)g.counters, (hipStream_t)stream);
   if (!B || !C) throw sc::Error{SC_ERR_ARG, "null device buffer"};
   int dev = -1;
   hip_check(hipGetDevice(&dev), "hipGetDevice");
   if (dev != p->device) throw sc::Error{SC_ERR_ARG, "plan lives on another device than the current one"};
   if ((uintptr_t)B % 16 || (uintptr_t)C % 16)
     throw sc::Error{SC_ERR_ARG, "B and C must be aligned to their vector width (16 B when N % 4 == 0)"};
+  if (clear && g.counters > 0) clear_counters(counters, (size_t)g.counters, (hipStream_t)stream);
   hip_check(sc::launch_band(p->band, g, B, C, work, counters, p->M, p->K, N, (flags & SC_ACCUMULATE) ? 1 : 0,
                             (hipStream_t)stream),
             "band kernel launch");
@@ -867,7 +908,11 @@ bool launch_band(const sc_plan *p, const float *B, float *C, int32_t N, int32_t 
 }
 
 // ---- the static scratch of sc_spmm_noalloc --------------------------------
-constexpr size_t kScratchWorkBytes = sc::kSplitWorkFloats * sizeof(float);
+// partial sums: the band kernel's at N = 128 on a 4096-row plan with 8 K
+// ranges (16 MiB), which also holds the tiled kernel's (kSplitWorkFloats)
+constexpr size_t kScratchWorkFloats = (size_t)4 << 20;
+static_assert(kScratchWorkFloats >= sc::kSplitWorkFloats, "the scratch holds the tiled kernel's workspace");
+constexpr size_t kScratchWorkBytes = kScratchWorkFloats * sizeof(float);
 constexpr size_t kScratchBytes = kScratchWorkBytes + sc::kSplitCounters * sizeof(unsigned);
 
 }  // namespace
@@ -938,11 +983,11 @@ int sc_plan_describe(const sc_plan *p, int32_t N, char *buf, size_t buflen) {
     if (!p || !buf || buflen == 0) throw sc::Error{SC_ERR_ARG, "null argument"};
     if (N < 1) throw sc::Error{SC_ERR_ARG, "N must be >= 1"};
     std::string d;
-    const sc::BandGeometry bg = sc::band_geometry(p->band, N);
+    const sc::BandGeometry bg = sc::band_geometry(p->band, N, p->band_work_floats, p->band_cnt_n);
     if (bg.use) {
-      d = "band_kernel km=4 cols=" + std::to_string(sc::kBandCols) + " tile_rows=" + std::to_string(p->band.KT) +
-          " bands=" + std::to_string(p->band.nbands) + " chunks=" + std::to_string(bg.nch) + " ks=" +
-          std::to_string(bg.nks) + " tiles_per_unit=" + std::to_string(bg.tpu) + " grid=" + std::to_string(bg.grid);
+      d = "band_kernel km=4 cols=" + std::to_string(sc::kBandCols) + " range_rows=" + std::to_string(p->band.KR) +
+          " bands=" + std::to_string(p->band.nbands) + " ks=" + std::to_string(p->band.nks) + " chunks=" +
+          std::to_string(bg.nch) + " grid=" + std::to_string(bg.grid);
       if (d.size() + 1 > buflen) throw sc::Error{SC_ERR_ARG, "buffer too small"};
       std::memcpy(buf, d.c_str(), d.size() + 1);
       return;
@@ -989,7 +1034,7 @@ int sc_spmm(const sc_plan *plan, const float *dB, float *dC, int32_t N, int32_t 
     if (flags & ~SC_ACCUMULATE) throw sc::Error{SC_ERR_ARG, "unknown flags"};
     if (!plan) throw sc::Error{SC_ERR_ARG, "null plan"};
     if (N >= 1 && launch_band(plan, dB, dC, N, flags, hip_stream, plan->band_work, plan->band_cnt,
-                              sc::kBandWorkFloats))
+                              plan->band_work_floats, plan->band_cnt_n))
       return;
     if (N >= 1) plan = layout_for(plan, N);
     launch(plan, plan->gen.rec, (sc_gen_launch_fn)plan->gen.launch, dB, dC, N, flags, waves_per_panel, hip_stream);
@@ -1006,17 +1051,19 @@ int sc_spmm_noalloc(const sc_plan *plan, const float *dB, float *dC, int32_t N, 
     if (dev != plan->device) throw sc::Error{SC_ERR_ARG, "plan lives on another device than the current one"};
     unsigned char *base = scratch_base(dev);
     const Scratch sc{(float *)base, sc::kSplitWorkFloats, (unsigned *)(base + kScratchWorkBytes), sc::kSplitCounters};
-    // the split-K kernels size their K split to fit this scratch (the plan
-    // workspace has the same size, so the launches match sc_spmm's); a
-    // geometry that needed more would be refused here
+    // the tiled kernel sizes its K split to the plan's workspace, which this
+    // scratch holds, so its launches match sc_spmm's; the band kernel's K
+    // split is the plan's, and a launch whose partial sums or counters exceed
+    // the scratch is refused
     if (N >= 1 && plan->band.img) {
-      const sc::BandGeometry g = sc::band_geometry(plan->band, N, sc::kBandTargetUnits, sc.work_floats);
-      if (g.use && (g.work_floats > sc.work_floats || (size_t)g.counters > sc.counters_n))
+      const sc::BandGeometry want = sc::band_geometry(plan->band, N, plan->band_work_floats, plan->band_cnt_n);
+      if (want.use && (want.work_floats > kScratchWorkFloats || (size_t)want.counters > sc::kSplitCounters))
         throw sc::Error{SC_ERR_UNSUPPORTED, "the band kernel would need more than the " +
                                                 std::to_string(kScratchBytes) + "-byte static scratch"};
+      if (want.use && launch_band(plan, dB, dC, N, flags, hip_stream, sc.work, sc.counters, kScratchWorkFloats,
+                                  sc::kSplitCounters, true))
+        return;
     }
-    if (N >= 1 && launch_band(plan, dB, dC, N, flags, hip_stream, sc.work, sc.counters, sc.work_floats, true))
-      return;
     if (N >= 1) plan = layout_for(plan, N);
     launch(plan, plan->gen.rec, (sc_gen_launch_fn)plan->gen.launch, dB, dC, N, flags, waves_per_panel, hip_stream,
            &sc);

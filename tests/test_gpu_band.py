@@ -1,8 +1,8 @@
 """GPU parity of the band kernel (SC_PLAN_BANDS, kernel_m 4, N a multiple of
-64): B staged in LDS per band of 128 rows and K tile, every slot on the
-matrix cores (four slots of one panel to an item, whatever their patterns),
-split K with the plan's workspace.  Against the CPU oracle on the same
-inputs.
+64): B staged in LDS once per (band of panels, K range of up to 512 rows),
+every slot on the matrix cores (four slots of one panel to an item, whatever
+their patterns), split K over the ranges with the plan's workspace.  Against
+the CPU oracle on the same inputs.
 
 Floating point: max relative error <= 1e-5 normalised by (|A| |B|)_ij
 against the fp64 product of the same fp32 operands (with accumulate, by
@@ -50,12 +50,12 @@ def test_band_structured_4096(n):
 
 
 @pytest.mark.parametrize("shape,density,n", [
-    ((512, 512), 0.10, 64),      # 4 bands, K in two tiles: two K ranges
-    ((1000, 700), 0.20, 128),    # ragged bands (last panel and band partial), ragged last K tile
-    ((37, 53), 0.30, 64),        # one band, one panel row short, one tile
+    ((512, 512), 0.10, 64),      # 8 bands of 16 panels, one K range
+    ((1000, 700), 0.20, 128),    # ragged last band and panel, two K ranges, the last short
+    ((37, 53), 0.30, 64),        # one band, one panel row short, one K range
     ((2048, 512), 0.50, 128),    # FFN shapes
     ((512, 2048), 0.10, 192),    # three N chunks
-    ((256, 4096), 0.02, 64),     # long K: many tiles per unit
+    ((256, 4096), 0.02, 64),     # long K: eight K ranges
 ])
 def test_band_uniform_shapes(shape, density, n):
     m, k = shape
@@ -112,20 +112,33 @@ def test_band_falls_back_off_its_shapes():
     assert err <= REL_TOL
 
 
-def test_band_falls_back_when_a_unit_would_hold_more_than_63_tiles():
-    # 64 bands x 4 chunks at N = 256 leave no room to split K, so a unit would
-    # hold all 79 K tiles, more than its image offsets' 64 lanes: the plan runs
-    # its other kernels; at N = 64 (4 K ranges of 20 tiles) it runs the band
-    # kernel
-    A, _ = synth_case(8192, 20000, 0.0005, 1, seed=0x5EED0000 + 7400)
-    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1), BANDS)
-    assert "tile_rows=256" in plan.describe(64), plan.describe(64)
-    assert not plan.describe(256).startswith("band_kernel"), plan.describe(256)
+def test_band_falls_back_beyond_sixteen_k_ranges():
+    # K = 20000 needs 40 K ranges of 512 rows: the plan builds no band layout
+    # and runs its other kernels; K = 8000 (16 ranges, the last one short)
+    # runs the band kernel with its split K over all sixteen
     rng = np.random.default_rng(9)
-    for n in (64, 256):
-        B = rng.uniform(-1, 1, size=(20000, n)).astype(np.float32)
+    for k, band in ((20000, False), (8000, True)):
+        A, _ = synth_case(1024, k, 0.002, 1, seed=0x5EED0000 + 7400 + k)
+        plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1), BANDS)
+        assert plan.describe(64).startswith("band_kernel") == band, plan.describe(64)
+        if band:
+            assert "ks=16" in plan.describe(64), plan.describe(64)
+        B = rng.uniform(-1, 1, size=(k, 64)).astype(np.float32)
         err, _ = oracle_check(A, B, run(plan, B))
-        assert err <= REL_TOL, (n, err)
+        assert err <= REL_TOL, (k, err)
+
+
+def test_band_wave_balance_shapes():
+    # bands of 16 to 128 panels (1 to 8 a wave), panels with no slot in a K
+    # range, a band whose last panel is short, and waves without panels
+    rng = np.random.default_rng(11)
+    for m, k, dens in ((4096, 8192, 0.01), (2052, 3000, 0.03), (64, 1100, 0.05), (8, 600, 0.2)):
+        A, _ = synth_case(m, k, dens, 1, seed=0x5EED0000 + 7500 + m)
+        plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1), BANDS)
+        assert plan.describe(128).startswith("band_kernel"), plan.describe(128)
+        B = rng.uniform(-1, 1, size=(k, 128)).astype(np.float32)
+        err, _ = oracle_check(A, B, run(plan, B))
+        assert err <= REL_TOL, (m, k, err)
 
 
 def test_band_empty_matrix_overwrites_c():

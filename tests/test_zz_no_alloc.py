@@ -37,7 +37,7 @@ def both(plan, B, C0=None):
 
 @pytest.mark.parametrize("flags", [sc_amd.PLAN_BANDS, sc_amd.PLAN_TILED])
 def test_noalloc_matches_spmm_two_calls(flags):
-    # first call: the 4096^2 headline matrix, K split four ways
+    # first call: the 4096^2 headline matrix, K split over several ranges
     A, B = synth_case(4096, 4096, 0.10, 128, seed=0x5EED0000 + 4128, structured=True)
     plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1), flags)
     kernel = plan.describe(128)
