@@ -1,6 +1,6 @@
 // sc_band.hpp -- the band kernel: kernel_m 4 plans at N a multiple of 64,
-// with B staged in LDS once per (band of panels, K range) and every slot on
-// the matrix cores.
+// with B staged in LDS once per (band of panels, K range) and every stored
+// entry on the matrix cores.
 //
 // Why.  The panel kernels gather one B row per slot from L2 (a 512-byte row
 // at N = 128); on a 4096 x 4096 matrix at 10 % density that is 415 MB per
@@ -12,41 +12,44 @@
 //
 // Work decomposition.  A unit (workgroup of 16 waves) owns one band, one N
 // chunk of 64 columns and one K range of up to 512 B rows.  It stages
-// B[range rows, chunk] (256 bytes a row, then one row of zeros for padding
-// slots) in LDS by LDS DMA, waits once, and then its waves run on their own:
-// no barrier couples them.  The plan assigns the band's panels to the 16
-// waves per K range, balancing their items (longest first onto the least
-// loaded wave); a wave runs its panels one after another, accumulating each
-// in registers, and hands it over when its items end.  The unit count is
-// bands x K ranges x N chunks; consecutive units take consecutive K ranges,
-// so with 8 K ranges every XCD holds one range of B and the two chunks of a
-// (band, range) share the stream in one L2.
+// B[range rows, chunk] (256 bytes a row) in LDS by LDS DMA, waits once, and
+// then its waves run on their own: no barrier couples them.  The plan
+// assigns the band's panels to the 16 waves per K range, balancing their
+// items (longest first onto the least loaded wave); a wave runs its panels
+// one after another, accumulating each in registers, and keeps the finished
+// tiles in registers until its last panel.  The unit count is bands x K
+// ranges x N chunks; consecutive units take consecutive K ranges, so with 8
+// K ranges every XCD holds one range of B and the two chunks of a (band,
+// range) share the stream in one L2.
 //
-// Items on the matrix cores.  A panel's slots in the range, in column order,
-// come four to an item, whatever their patterns (rows a pattern lacks carry
-// value 0), and every item runs on v_mfma_f32_4x4x1f32: 16 blocks of a 4-row
-// by 4-column outer product; block b = 4s + c takes slot s and columns
-// 16c + 4j + q (j the block's column, q = 0..3 over four instructions).
-// Lane 16s + 4c + j reads 16 bytes at column 16c + 4j of slot s's staged B
-// row (one LDS read feeds the four instructions).  A wave's items, all its
-// panels one after another, come in blocks of 16 items (four groups of
-// four), 320 dwords each:
+// Items on the matrix cores.  An item is a window of four consecutive
+// columns of A (four consecutive B rows, aligned to 4 in the range) inside
+// one panel: its 16 values, row i and column t at A(i, t), 0 where no entry
+// is stored.  It runs as four v_mfma_f32_4x4x1f32, instruction t taking
+// window column t: all 16 blocks take its four row values (cbsz 4, abid the
+// lane block holding them) and block b columns 4b .. 4b + 3 of B row
+// (window + t), so lane l reads the one float at column l of each of the
+// four rows (ds_read_b32 at offsets 0, 256, 512, 768 from one address), and
+// instruction t accumulates into the 4 x 64 tile D[t]: lane l holds rows
+// 0..3 of column l.  The four tiles are added in the lane when the panel
+// ends; there is no cross-lane reduction.  A wave's items,
+// all its panels one after another, come in blocks of 16 items (four groups
+// of four), 272 dwords each:
 //   * 256 values: lane l loads the 16 bytes at 4l, whose dword G is
-//     value (item 4G + t, slot s, row i) for l = 16s + 4t + i; item 4G + t's
-//     instructions take their A operand from dword G with cbsz 2 / abid t
-//     (each group of four blocks reads block 4s + t's lanes), so no lane
-//     holds a copy;
-//   * 64 B-row byte offsets into the stage, (item x, slot s) at 16s + x:
-//     lane l loads dword l, and item x's offset reaches the whole row of 16
-//     lanes by a DPP row broadcast (row_newbcast x).
-// Four blocks are in registers at a time: three load while one runs.
-// The four slot positions' sums are added once per panel with the gfx950
-// lane swaps (a reduce-scatter: lane 16s + x ends with row s).
+//     A(i, t) of item 4G + u for l = 16u + 4t + i;
+//   * 16 window byte offsets into the stage (item x at x), which lane
+//     16r + x loads, and item x's reaches the whole row of 16 lanes by a DPP
+//     row broadcast (row_newbcast x) fused with the add of the lane's column.
+// That one add is the only vector ALU work of an item: on gfx950 each VALU
+// instruction among 4x4x1 MFMAs costs about 1.5 MFMA issue slots (measured),
+// so the loop keeps them to one per four MFMAs.  Four blocks are in
+// registers at a time: three load while one runs.
 //
-// Numerics.  Rows a slot's pattern lacks are multiplied by 0 here, as the
-// format's own padding slots are in the reference's kernels: with finite B
-// the sums equal the pattern bodies' to rounding, while an Inf or NaN in a B
-// row can reach a row of C that has no entry in that column (0 * Inf = NaN).
+// Numerics.  A window's zero values multiply B rows the panel's row does not
+// use, as the format's own padding slots do in the reference's kernels: with
+// finite B the sums equal the pattern bodies' to rounding, while an Inf or
+// NaN in a B row can reach a row of C that has no entry in that column
+// (0 * Inf = NaN).
 //
 // Split K.  With more than one K range, a wave writes each panel's partial
 // tile (4 rows x 64 columns) to the workspace with write-through stores and,
@@ -70,7 +73,7 @@ constexpr int kBandCols = 64;                 // columns of B and C per N chunk
 constexpr int kBandRowBytes = 4 * kBandCols;  // bytes of one staged B row
 constexpr int kBandMaxRange = 512;            // most B rows of one K range
 constexpr int kBandMaxRanges = 16;            // most K ranges (K up to 8192)
-constexpr int kBandBlockDw = 320;             // dwords of a block of 16 items (4 groups)
+constexpr int kBandBlockDw = 272;             // dwords of a block of 16 items (4 groups)
 constexpr int kBandRecHeader = 4;             // dwords of a wave record's header
 constexpr int kBandWavePanels = 8;            // most panels of one wave per K range
 constexpr int kBandBlocksInFlight = 4;        // stream blocks a wave holds in registers
@@ -86,15 +89,15 @@ constexpr int kBandTargetPairs = 128;
 //   (at least one), [3] 0;
 //   then np (panel, groups) pairs, padded to a multiple of 4 dwords;
 //   then the blocks (layout above), the panels' groups one after another.
-//   A panel's last group is padded with items of value 0 on the zero row, the
-//   last block with such groups; a panel with no slot in the range has one
+//   A panel's last group is padded with items of value 0 on window 0, the
+//   last block with such groups; a panel with no entry in the range has one
 //   such group, and a wave without panels one block of them.
 struct BandView {
   const int *img;   // wave records
   const int *woff;  // first dword of record (band * nks + ks) * 16 + w, + end
   int nbands;
   int nks;          // K ranges
-  int KR;           // B rows per K range (a multiple of 4; the zero row follows)
+  int KR;           // B rows per K range (a multiple of 4)
   int npanels;
 };
 
@@ -108,7 +111,7 @@ struct BandGeometry {
   int counters = 0;        // arrival counters needed (nks > 1)
 };
 
-__host__ __device__ inline size_t band_lds_bytes(int KR) { return (size_t)(KR + 1) * kBandRowBytes; }
+__host__ __device__ inline size_t band_lds_bytes(int KR) { return (size_t)KR * kBandRowBytes; }
 
 // Partial tile (4 x 64 floats) of (K range k, panel q, chunk c).
 __host__ __device__ inline size_t band_partial_floats(int nks, int npanels, int nch) {
@@ -136,32 +139,41 @@ inline BandGeometry band_geometry(const BandView &b, int N, size_t work_cap, siz
 typedef float vec4f_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) char lds_char;
 
-// Swap halves between two registers: x's lanes 32..63 with y's lanes 0..31
-// (v_permlane32_swap_b32), and x's rows 1 and 3 with y's rows 0 and 2
-// (v_permlane16_swap_b32).  Inline asm for the reason given at lane_down;
-// the s_nop covers the VALU-write hazard.
-__device__ __forceinline__ void swap_halves32(float &x, float &y) {
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(y));
-}
-__device__ __forceinline__ void swap_rows16(float &x, float &y) {
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+// The four B values of one item for this lane: column `lane` of the
+// window's rows (window offset W broadcast from lane 16r + X of every row,
+// plus the lane's column bytes `lc`).
+struct BandRows {
+  float x[4];
+};
+
+template <int X>
+__device__ __forceinline__ BandRows band_read(const lds_char *lds, int W, int lc) {
+  const int a = __builtin_amdgcn_update_dpp(0, W, 0x150 + X, 0xf, 0xf, false) + lc;
+  const lds_char *p = lds + a;
+  BandRows r;
+  r.x[0] = *(const lds_float *)(p);
+  r.x[1] = *(const lds_float *)(p + kBandRowBytes);
+  r.x[2] = *(const lds_float *)(p + 2 * kBandRowBytes);
+  r.x[3] = *(const lds_float *)(p + 3 * kBandRowBytes);
+  return r;
 }
 
-// Item T of a group: its B rows (offset o, broadcast from lane 16s + T of
-// every row), then the four instructions.
-template <int T>
-__device__ __forceinline__ vec4f band_read(const lds_char *tile, int o) {
-  const int off = __builtin_amdgcn_update_dpp(0, o, 0x150 + T, 0xf, 0xf, false);
-  return *(const lds_float4 *)(tile + off);
+// Item 4G + U: its four instructions; window column t's row values sit in
+// lane block 4U + t of values dword G.
+// Window column t accumulates into D[t], so consecutive instructions do not
+// wait on each other's results; the four are added when the panel ends.
+template <int U>
+__device__ __forceinline__ void band_mfma(vec4f_t (&D)[4], float a, const BandRows &r) {
+  D[0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, r.x[0], D[0], 4, 4 * U + 0, 0);
+  D[1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, r.x[1], D[1], 4, 4 * U + 1, 0);
+  D[2] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, r.x[2], D[2], 4, 4 * U + 2, 0);
+  D[3] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, r.x[3], D[3], 4, 4 * U + 3, 0);
 }
 
-template <int T>
-__device__ __forceinline__ void band_mfma(vec4f_t (&D)[4], float a, const vec4f &x) {
-  D[0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, x.x, D[0], 2, T, 0);
-  D[1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, x.y, D[1], 2, T, 0);
-  D[2] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, x.z, D[2], 2, T, 0);
-  D[3] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, x.w, D[3], 2, T, 0);
-}
+// The B values of one group's four items.
+struct BandGroupRows {
+  BandRows it[4];
+};
 
 // The band kernel (kernel_m 4).  blockDim.x = 64 * kBandWaves.  Unit u of
 // the grid: ks = u % nks, chunk = (u / nks) % nch, band = u / (nks * nch).
@@ -181,12 +193,11 @@ __global__ void __launch_bounds__(64 * kBandWaves)
   const int rows = min(KR, K - k0);
   lds_char *lds = (lds_char *)smem4;
 
-  // the zero row (row KR): padding slots read it
-  if (threadIdx.x < kBandCols / 4) ((lds_float4 *)(lds + KR * kBandRowBytes))[threadIdx.x] = vec4f{0.f, 0.f, 0.f, 0.f};
   // B[k0 .. k0 + rows, n0 .. n0 + 64) into LDS by LDS DMA: one wave
   // instruction moves four B rows (lane l: row l / 16 of the four, 16 bytes
   // of column group l % 16), wave w the groups w, w + 16, ...; rows past the
-  // range re-read its last row into rows below KR (never referenced)
+  // range re-read its last row into rows below KR (read by windows that
+  // reach past the range, whose values there are 0)
   {
     const int groups = (rows + 3) >> 2;
     const float *src = B + n0 + (lane & 15) * 4;
@@ -203,7 +214,6 @@ __global__ void __launch_bounds__(64 * kBandWaves)
   // access but the stream's block loads
   const int *rec = img + woff[(band * nks + ks) * kBandWaves + w];
   const int npan = rec[0];
-  const int ngroups = rec[1];
   const int *ptab = rec + kBandRecHeader;
   const int *blk = ptab + ((2 * npan + 3) & ~3);
   const int nblk = rec[2];
@@ -212,38 +222,44 @@ __global__ void __launch_bounds__(64 * kBandWaves)
     pidv = ptab[2 * lane];
     ngv = ptab[2 * lane + 1];
   }
-  const vec4f *bval = reinterpret_cast<const vec4f *>(blk) + lane;
-  const int *boff = blk + 256 + lane;
+  // the blocks through a buffer descriptor: the block's byte offset is a
+  // scalar, the lane's part a constant, so a block load costs no vector
+  // address arithmetic (non-temporal: the stream is read once)
+  const __amdgpu_buffer_rsrc_t brs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int *>(blk), (short)0, (int)0x7fffffff, kBufferWord3);
+  const unsigned vofs = 16u * (unsigned)lane;
+  const unsigned wofs = 4u * (256u + (unsigned)(lane & 15));
+  auto load_block = [&](int nb, vec4f &Vv, int &Wv) __attribute__((always_inline)) {
+    const unsigned so = (unsigned)__builtin_amdgcn_readfirstlane(nb * kBandBlockDw * 4);
+    Vv = __builtin_bit_cast(vec4f, __builtin_amdgcn_raw_buffer_load_b128(brs, vofs, so, kCachePolicyNt));
+    Wv = (int)__builtin_amdgcn_raw_buffer_load_b32(brs, wofs, so, kCachePolicyNt);
+  };
   // blocks b .. b + 3 in registers (the stream comes from HBM: three blocks
   // of lead time cover its latency under load).  Every record holds at least
   // one block, so the four loads are issued on every path (past the end they
   // re-read the last block), and the barrier waits for the DMA and the panel
   // table only: the blocks keep arriving while the first groups run.
   vec4f V[kBandBlocksInFlight];
-  int O[kBandBlocksInFlight];
+  int W[kBandBlocksInFlight];
 #pragma unroll
   for (int i = 0; i < kBandBlocksInFlight; ++i) {
     const int nb = min(i, nblk - 1);
-    V[i] = __builtin_nontemporal_load(bval + (size_t)nb * (kBandBlockDw / 4));
-    O[i] = __builtin_nontemporal_load(boff + (size_t)nb * kBandBlockDw);
+    load_block(nb, V[i], W[i]);
   }
   // vmcnt(8): everything but the eight block loads (the DMA, the panel
-  // table); expcnt and lgkmcnt at their maximum (no wait; the barrier below
-  // waits for the LDS writes of the zero row)
+  // table); expcnt and lgkmcnt at their maximum (no wait)
   static_assert(kBandBlocksInFlight * 2 == 8, "the wait below counts eight block loads");
   __builtin_amdgcn_s_waitcnt(0x0F78);
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the zero row is written
   // a bare barrier: __syncthreads() would also wait for the block loads
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
-  // this lane's 16 bytes (columns 16c + 4j .. + 3) of a staged row; the
-  // offsets in the stream add to it
-  const lds_char *tile = lds + 16 * (lane & 15);
+  // this lane's column of a staged row; the windows' offsets add to it
+  const int lc = 4 * lane;
   vec4f_t D[4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) D[q] = vec4f_t{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < 4; ++t) D[t] = vec4f_t{0.f, 0.f, 0.f, 0.f};
   // the wave's finished panel tiles (panel k in T[k]), stored after the loop:
   // a store pending beside the block loads would make every wait for a block
   // a wait for everything
@@ -251,23 +267,13 @@ __global__ void __launch_bounds__(64 * kBandWaves)
 #pragma unroll
   for (int k = 0; k < kBandWavePanels; ++k) T[k] = vec4f{0.f, 0.f, 0.f, 0.f};
 
-  // Panel p's tile is done: its four slot positions' sums (rows 0, 1 to
-  // lanes 0..31 and 2, 3 to lanes 32..63, then row 2 (s / 2) to the even
-  // rows of 16 lanes and 2 (s / 2) + 1 to the odd ones: lane 16s + x ends
-  // with row s) into T[p]
+  // Panel p's tile is done: lane l holds rows 0..3 of its column l.
   int p = 0;
   auto flush = [&]() __attribute__((always_inline)) {
-    vec4f r;
+    const vec4f_t d = (D[0] + D[1]) + (D[2] + D[3]);
+    const vec4f r = vec4f{d[0], d[1], d[2], d[3]};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float x0 = D[q][0], x2 = D[q][2], x1 = D[q][1], x3 = D[q][3];
-      swap_halves32(x0, x2);
-      swap_halves32(x1, x3);
-      float a = x0 + x2, b = x1 + x3;
-      swap_rows16(a, b);
-      r[q] = a + b;
-      D[q] = vec4f_t{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int t = 0; t < 4; ++t) D[t] = vec4f_t{0.f, 0.f, 0.f, 0.f};
     switch (p) {
 #define SC_BAND_KEEP(k) \
   case k:               \
@@ -288,68 +294,87 @@ __global__ void __launch_bounds__(64 * kBandWaves)
     ++p;
     if (p < npan) left = __builtin_amdgcn_readlane(ngv, p);
   };
-  // group G of a block (values dword G, offsets of items 4G .. 4G + 3)
-  auto group = [&](auto GC, const vec4f &V, int O) __attribute__((always_inline)) {
+  // Group G of a block: the B values of its items 4G .. 4G + 3 (windows in
+  // W), then their instructions (values dword G of V).  The reads of the
+  // next group are issued before a group's instructions, so a wave always
+  // has B values in flight while its instructions issue.
+  auto reads = [&](auto GC, int Wb) __attribute__((always_inline)) {
+    constexpr int G = decltype(GC)::value;
+    BandGroupRows x;
+    x.it[0] = band_read<4 * G + 0>(lds, Wb, lc);
+    x.it[1] = band_read<4 * G + 1>(lds, Wb, lc);
+    x.it[2] = band_read<4 * G + 2>(lds, Wb, lc);
+    x.it[3] = band_read<4 * G + 3>(lds, Wb, lc);
+    return x;
+  };
+  auto compute = [&](auto GC, const vec4f &V, const BandGroupRows &x) __attribute__((always_inline)) {
     constexpr int G = decltype(GC)::value;
     if (p >= npan) return;  // past the last panel: padding groups
-    const float v = V[G];
-    const vec4f x0 = band_read<4 * G + 0>(tile, O);
-    const vec4f x1 = band_read<4 * G + 1>(tile, O);
-    const vec4f x2 = band_read<4 * G + 2>(tile, O);
-    const vec4f x3 = band_read<4 * G + 3>(tile, O);
-    __builtin_amdgcn_sched_barrier(0);  // the four reads in flight together
-    band_mfma<0>(D, v, x0);
-    band_mfma<1>(D, v, x1);
-    band_mfma<2>(D, v, x2);
-    band_mfma<3>(D, v, x3);
+    const float a = V[G];
+    band_mfma<0>(D, a, x.it[0]);
+    band_mfma<1>(D, a, x.it[1]);
+    band_mfma<2>(D, a, x.it[2]);
+    band_mfma<3>(D, a, x.it[3]);
     if (--left == 0) {
       flush();
       next_panel();
     }
   };
-  auto run_block = [&](const vec4f &V, int O) __attribute__((always_inline)) {
-    group(std::integral_constant<int, 0>{}, V, O);
-    group(std::integral_constant<int, 1>{}, V, O);
-    group(std::integral_constant<int, 2>{}, V, O);
-    group(std::integral_constant<int, 3>{}, V, O);
-  };
+  using G0 = std::integral_constant<int, 0>;
+  using G1 = std::integral_constant<int, 1>;
+  using G2 = std::integral_constant<int, 2>;
+  using G3 = std::integral_constant<int, 3>;
   // The next loads are issued on every path (past the end they re-read the
   // last block), so that every wait for a block counts the same loads after
   // it; a load issued on one path only makes the compiler wait for
   // everything.  Blocks past the last one run no group (p == npan).
+  BandGroupRows x = reads(G0{}, W[0]);
   for (int b = 0; b < nblk; b += kBandBlocksInFlight) {
 #pragma unroll
     for (int i = 0; i < kBandBlocksInFlight; ++i) {
-      run_block(V[i], O[i]);
+      BandGroupRows y = reads(G1{}, W[i]);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(G0{}, V[i], x);
+      x = reads(G2{}, W[i]);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(G1{}, V[i], y);
+      y = reads(G3{}, W[i]);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(G2{}, V[i], x);
+      // the next block's first group (block b + 4 when i = 3: refilled at i = 0)
+      x = reads(G0{}, W[(i + 1) % kBandBlocksInFlight]);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(G3{}, V[i], y);
       const int nb = min(b + i + kBandBlocksInFlight, nblk - 1);
-      V[i] = __builtin_nontemporal_load(bval + (size_t)nb * (kBandBlockDw / 4));
-      O[i] = __builtin_nontemporal_load(boff + (size_t)nb * kBandBlockDw);
+      load_block(nb, V[i], W[i]);
     }
   }
 
   // the tiles to C (one K range) or as this range's partials to the
-  // workspace (written through, sc1); lane 16s + x holds row s, columns
-  // n0 + 4x .. + 3 of its panel
-  const int my_row = lane >> 4;
-  const int my_col = n0 + 4 * (lane & 15);
+  // workspace (written through, sc1, 16 bytes a lane: whole 128-byte lines);
+  // lane l holds rows 0..3 of column n0 + l of its panel
+  const int my_col = n0 + lane;
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(work, (short)0, (int)0x7fffffff, kBufferWord3);
+  auto to_c = [&](int pid, vec4f r) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 4 * pid + i;
+      if (row < M) {
+        float *dst = C + (size_t)row * N + my_col;
+        *dst = accumulate ? *dst + r[i] : r[i];
+      }
+    }
+  };
 #pragma unroll
   for (int k = 0; k < kBandWavePanels; ++k) {
     if (k >= npan) break;
     const int pid = __builtin_amdgcn_readlane(pidv, k);
-    vec4f r = T[k];
     if (nks == 1) {
-      const int row = 4 * pid + my_row;
-      if (row < M) {
-        vec4f *dst = reinterpret_cast<vec4f *>(C + (size_t)row * N + my_col);
-        if (accumulate) r += *dst;
-        *dst = r;
-      }
+      to_c(pid, T[k]);
     } else {
-      // 16 bytes a lane, so the wave writes whole 128-byte lines
       const unsigned off = (unsigned)((((size_t)ks * npanels + pid) * nch + chunk) * (4 * kBandCols) * sizeof(float)) +
                            16u * (unsigned)lane;
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(vec4i, r), wr, off, 0, kCachePolicySc1);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(vec4i, T[k]), wr, off, 0, kCachePolicySc1);
     }
   }
   if (nks == 1) return;
@@ -381,12 +406,7 @@ __global__ void __launch_bounds__(64 * kBandWaves)
         sum += __builtin_bit_cast(vec4f, __builtin_amdgcn_raw_buffer_load_b128(wr, off, (unsigned)(k * kstride),
                                                                                kCachePolicySc1));
       }
-      const int row = 4 * q + my_row;
-      if (row < M) {
-        vec4f *dst = reinterpret_cast<vec4f *>(C + (size_t)row * N + my_col);
-        if (accumulate) sum += *dst;
-        *dst = sum;
-      }
+      to_c(q, sum);
       if (lane == 0)
         __hip_atomic_store(counters + (size_t)q * nch + chunk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }

@@ -39,6 +39,8 @@ constexpr int kBufferWord3 = 0x00020000;
 // Cache-policy operand of the buffer-load builtins: SC1 (system coherence
 // bit of gfx940-family loads and stores).
 constexpr int kCachePolicySc1 = 16;
+// Cache-policy operand: NT (non-temporal: the line is not kept for reuse).
+constexpr int kCachePolicyNt = 2;
 
 // Clang vector types (HIP's float2/float4 classes cannot be assigned in
 // LDS address space 3).

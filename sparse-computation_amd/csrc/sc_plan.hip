@@ -649,9 +649,11 @@ std::vector<BandPanel> band_panels(const sc::Cfmtx &cf, const std::vector<PatInf
 // The wave records (layout: sc_band.hpp, BandView).  K ranges of up to
 // kBandMaxRange rows; bands of one to kBandWavePanels panels per wave, sized
 // so that bands x K ranges is about kBandTargetPairs; per (band, K range)
-// the panels go to the waves longest first, each onto the least loaded wave
-// that holds fewer than kBandWavePanels (load: its groups plus one per panel
-// for the hand-over), and a wave runs its panels in ascending order.
+// a panel's items are the windows of four consecutive columns (aligned to 4
+// in the range) that hold its entries, and the panels go to the waves
+// longest first, each onto the least loaded wave that holds fewer than
+// kBandWavePanels (load: its groups plus one per panel for the hand-over);
+// a wave runs its panels in ascending order.
 void band_records(const std::vector<BandPanel> &panels, int32_t K, BandHost &h) {
   const int32_t npanels = (int32_t)panels.size();
   h = BandHost{};
@@ -661,14 +663,18 @@ void band_records(const std::vector<BandPanel> &panels, int32_t K, BandHost &h) 
   const int32_t P = (int32_t)std::min<int64_t>((int64_t)sc::kBandWaves * sc::kBandWavePanels,
                                                std::max<int64_t>(sc::kBandWaves, want));
   h.nbands = (npanels + P - 1) / P;
-  const int32_t zero_off = h.KR * sc::kBandRowBytes;  // byte offset of the zero row
-  // a cursor into each panel's slots: its K ranges are visited in order
+  // a cursor into each panel's column-sorted slots: its K ranges are visited
+  // in order
   std::vector<size_t> cur((size_t)npanels, 0);
   h.woff.reserve((size_t)h.nbands * h.nks * sc::kBandWaves + 1);
+  struct Window {
+    int32_t w;      // window index in the range (B rows 4w .. 4w + 3)
+    float v[16];    // A(i, t) at 4t + i
+  };
   std::vector<int32_t> rec;
   for (int b = 0; b < h.nbands; ++b) {
     const int32_t q0 = b * P, q1 = std::min(npanels, q0 + P), nq = q1 - q0;
-    std::vector<size_t> c0((size_t)nq), c1((size_t)nq);
+    std::vector<std::vector<Window>> win((size_t)nq);
     std::vector<int32_t> ngr((size_t)nq), order((size_t)nq);
     for (int ks = 0; ks < h.nks; ++ks) {
       const int32_t klo = ks * h.KR;
@@ -676,14 +682,22 @@ void band_records(const std::vector<BandPanel> &panels, int32_t K, BandHost &h) 
       for (int32_t i = 0; i < nq; ++i) {
         const BandPanel &bp = panels[(size_t)(q0 + i)];
         size_t &c = cur[(size_t)(q0 + i)];
-        c0[(size_t)i] = c;
+        std::vector<Window> &ws = win[(size_t)i];
+        ws.clear();
         while (c < bp.slots.size() && bp.slots[c].first < khi) {
-          if (bp.slots[c].first < klo) throw sc::Error{SC_ERR_INTERNAL, "band layout lost a slot"};
+          const int32_t col = bp.slots[c].first;
+          if (col < klo) throw sc::Error{SC_ERR_INTERNAL, "band layout lost a slot"};
+          const int32_t wi = (col - klo) >> 2, t = (col - klo) & 3;
+          if (ws.empty() || ws.back().w != wi) ws.push_back(Window{wi, {0.f}});
+          for (int r = 0; r < 4; ++r) {
+            float &dst = ws.back().v[4 * t + r];
+            if (dst != 0.f && bp.slots[c].second[(size_t)r] != 0.f)
+              throw sc::Error{SC_ERR_INTERNAL, "band layout met one entry twice"};
+            dst += bp.slots[c].second[(size_t)r];
+          }
           ++c;
         }
-        c1[(size_t)i] = c;
-        const size_t items = (c - c0[(size_t)i] + 3) / 4;
-        ngr[(size_t)i] = (int32_t)std::max<size_t>(1, (items + 3) / 4);  // an empty panel: one group of zeros
+        ngr[(size_t)i] = (int32_t)std::max<size_t>(1, (ws.size() + 3) / 4);  // an empty panel: one group of zeros
         order[(size_t)i] = i;
       }
       std::stable_sort(order.begin(), order.end(),
@@ -712,24 +726,21 @@ void band_records(const std::vector<BandPanel> &panels, int32_t K, BandHost &h) 
           rec[sc::kBandRecHeader + 2 * k] = q0 + mine[k];
           rec[sc::kBandRecHeader + 2 * k + 1] = ngr[(size_t)mine[k]];
         }
-        // every offset starts on the zero row (padding items and groups)
+        // padding items: values 0 on window 0
         const size_t base = sc::kBandRecHeader + ptab_dw;
-        for (size_t b = 0; b < nblk; ++b)
-          for (int l = 0; l < 64; ++l) rec[base + b * sc::kBandBlockDw + 256 + (size_t)l] = zero_off;
         size_t gi = 0;  // the wave's group index
         for (int32_t i : mine) {
-          const BandPanel &bp = panels[(size_t)(q0 + i)];
+          const std::vector<Window> &ws = win[(size_t)i];
           for (int32_t G = 0; G < ngr[(size_t)i]; ++G, ++gi) {
             int32_t *bk = &rec[base + (gi / 4) * sc::kBandBlockDw];
             const int g4 = (int)(gi % 4);
-            for (int t = 0; t < 4; ++t)
-              for (int s4 = 0; s4 < 4; ++s4) {
-                const size_t j = c0[(size_t)i] + 4 * (4 * (size_t)G + t) + s4;
-                if (j >= c1[(size_t)i]) continue;
-                bk[256 + 16 * s4 + 4 * g4 + t] = (bp.slots[j].first - klo) * sc::kBandRowBytes;
-                for (int r = 0; r < 4; ++r)
-                  std::memcpy(&bk[4 * (16 * s4 + 4 * t + r) + g4], &bp.slots[j].second[(size_t)r], 4);
-              }
+            for (int u = 0; u < 4; ++u) {
+              const size_t m = 4 * (size_t)G + u;
+              if (m >= ws.size()) continue;
+              bk[256 + 4 * g4 + u] = ws[m].w * 4 * sc::kBandRowBytes;
+              for (int t = 0; t < 4; ++t)
+                for (int r = 0; r < 4; ++r) std::memcpy(&bk[4 * (16 * u + 4 * t + r) + g4], &ws[m].v[4 * t + r], 4);
+            }
           }
         }
         if ((int64_t)h.img.size() + (int64_t)rec.size() > INT32_MAX)
