@@ -125,12 +125,12 @@ void sc_cfmtx_free(sc_cfmtx *cf);
 #define SC_PLAN_PATTERNS 32    /* keep only the km-row pattern layout           */
 #define SC_PLAN_BANDS 64       /* kernel_m 4 files: also build the band layout (B
                                   staged in LDS once per band of panels and K
-                                  range of up to 512 rows, every slot on the
-                                  matrix cores, split K over the ranges with a
-                                  plan-owned workspace; the format's zero
-                                  padding slots are skipped; K up to 8192);
-                                  sc_spmm runs it at N a multiple of 64 up to
-                                  256                                           */
+                                  range of up to 512 rows, 4-column windows of
+                                  each panel on the matrix cores, split K over
+                                  the ranges with a plan-owned workspace; the
+                                  format's zero padding slots are skipped; K up
+                                  to 8192); sc_spmm runs it at N a multiple of
+                                  64 up to 256                                 */
 /* Without SC_PLAN_ROWS, SC_PLAN_PATTERNS, SC_PLAN_TILED or SC_PLAN_CHUNKED a
  * plan of a kernel_m > 1 file holds both layouts, and sc_spmm / sc_spmv run
  * the one-row layout while its B-row gathers (4 * stored entries * N bytes)
