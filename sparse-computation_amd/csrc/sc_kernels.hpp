@@ -1589,12 +1589,37 @@ __device__ __forceinline__ vec4f row_of(const float *__restrict__ B, int col) {
     return vec4f{B[col], 0.f, 0.f, 0.f};
   }
 }
-template <int ROWS, int V>
+template <int V>
+__device__ __forceinline__ vec4f row_of_lds(const lds_float *xs, int col) {
+  if constexpr (V == 4) return *(const lds_float4 *)(xs + col * 4);
+  else if constexpr (V == 2) {
+    const vec2f t = *(const lds_float2 *)(xs + col * 2);
+    return vec4f{t.x, t.y, 0.f, 0.f};
+  } else {
+    return vec4f{xs[col], 0.f, 0.f, 0.f};
+  }
+}
+// STAGE: the workgroup first copies all of B (K x V floats) into LDS and the
+// rows gather from there (kRowStagedRows rows a workgroup, so that a CU
+// copies B about once): on a plan with many entries per B row the gathers
+// then cost LDS reads instead of one L2 request each.
+template <int ROWS, int V, bool STAGE>
 __global__ void __launch_bounds__(64 * ROWS)
     row_spmv_kernel(const int *__restrict__ panel_slot, const int *__restrict__ panel_val,
                     const int *__restrict__ row_len, const int *__restrict__ cols,
                     const float *__restrict__ vals, const float *__restrict__ B, float *__restrict__ C, int M,
-                    int accumulate) {
+                    int K, int accumulate) {
+  extern __shared__ float4 xs4[];
+  lds_float *xs = (lds_float *)xs4;
+  if constexpr (STAGE) {
+    const int nf = K * V;
+    for (int i = threadIdx.x; i < nf; i += 64 * ROWS) xs[i] = B[i];
+    __syncthreads();
+  }
+  auto b_row = [&](int col) __attribute__((always_inline)) {
+    if constexpr (STAGE) return row_of_lds<V>(xs, col);
+    else return row_of<V>(B, col);
+  };
   const int row = blockIdx.x * ROWS + (int)(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= M) return;
@@ -1613,10 +1638,10 @@ __global__ void __launch_bounds__(64 * ROWS)
       const vec4i c = __builtin_nontemporal_load(c4 + q);
       const vec4f v = __builtin_nontemporal_load(v4 + q);
       const int e = q * 4;
-      const float x0 = B[c.x];  // e < n for every q < nq
-      const float x1 = e + 1 < n ? B[c.y] : 0.f;
-      const float x2 = e + 2 < n ? B[c.z] : 0.f;
-      const float x3 = e + 3 < n ? B[c.w] : 0.f;
+      const float x0 = b_row(c.x)[0];  // e < n for every q < nq
+      const float x1 = e + 1 < n ? b_row(c.y)[0] : 0.f;
+      const float x2 = e + 2 < n ? b_row(c.z)[0] : 0.f;
+      const float x3 = e + 3 < n ? b_row(c.w)[0] : 0.f;
       acc[0] = __builtin_fmaf(v.x, x0, acc[0]);
       if (e + 1 < n) acc[0] = __builtin_fmaf(v.y, x1, acc[0]);
       if (e + 2 < n) acc[0] = __builtin_fmaf(v.z, x2, acc[0]);
@@ -1628,10 +1653,10 @@ __global__ void __launch_bounds__(64 * ROWS)
     const vec4f v = __builtin_nontemporal_load(v4 + q);
     const int e = q * 4;
     const vec4f zero = {0.f, 0.f, 0.f, 0.f};
-    const vec4f b0 = row_of<V>(B, c.x);  // e < n for every q < nq
-    const vec4f b1 = e + 1 < n ? row_of<V>(B, c.y) : zero;
-    const vec4f b2 = e + 2 < n ? row_of<V>(B, c.z) : zero;
-    const vec4f b3 = e + 3 < n ? row_of<V>(B, c.w) : zero;
+    const vec4f b0 = b_row(c.x);  // e < n for every q < nq
+    const vec4f b1 = e + 1 < n ? b_row(c.y) : zero;
+    const vec4f b2 = e + 2 < n ? b_row(c.z) : zero;
+    const vec4f b3 = e + 3 < n ? b_row(c.w) : zero;
 #pragma unroll
     for (int k = 0; k < V; ++k) {
       acc[k] = __builtin_fmaf(v.x, b0[k], acc[k]);
@@ -1669,6 +1694,14 @@ inline bool use_row_spmv(const DevView &v, int km, int N, int W) {
   return km == 1 && (N == 1 || N == 2 || N == 4) && W == 1 && v.row_len != nullptr;
 }
 
+// ... and with B staged in LDS: B fits 32 KiB, the rows fill at least 256
+// workgroups of kRowStagedRows, and every B row serves at least 64 entries.
+constexpr int kRowStagedRows = 16;
+inline bool row_spmv_staged(const DevView &v, int N) {
+  return (long long)v.K * N * (long long)sizeof(float) <= 32768 && v.M >= 256 * kRowStagedRows &&
+         v.nslots >= 64ll * v.K;
+}
+
 // The buffer-descriptor form of the lanes-over-slots kernel forms a B-row
 // offset as __umul24(row, N * 4) + lane bytes: every operand of the 24-bit
 // multiply must fit 24 bits (K below 2^24 rows, N * 4 below 2^24 bytes) and
@@ -1689,13 +1722,22 @@ hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int 
                          int pack, hipStream_t stream) {
   if (v.npanels <= 0 || N <= 0) return hipSuccess;
   if (use_row_spmv(v, KM, N, W)) {
-    const dim3 rgrid((unsigned)((v.M + kRowSpmvRows - 1) / kRowSpmvRows)), rblock(64u * kRowSpmvRows);
-#define SC_ROW(VV)                                                                                       \
-  hipLaunchKernelGGL((row_spmv_kernel<kRowSpmvRows, VV>), rgrid, rblock, 0, stream, v.panel_slot,      \
-                     v.panel_val, v.row_len, v.cols, v.vals, B, C, v.M, accumulate)
-    if (N == 4) SC_ROW(4);
-    else if (N == 2) SC_ROW(2);
-    else SC_ROW(1);
+    const bool st = row_spmv_staged(v, N);
+    const int rows = st ? kRowStagedRows : kRowSpmvRows;
+    const size_t lds = st ? (size_t)v.K * N * sizeof(float) : 0;
+    const dim3 rgrid((unsigned)((v.M + rows - 1) / rows)), rblock(64u * rows);
+#define SC_ROW(RR, VV, SS)                                                                              \
+  hipLaunchKernelGGL((row_spmv_kernel<RR, VV, SS>), rgrid, rblock, lds, stream, v.panel_slot,         \
+                     v.panel_val, v.row_len, v.cols, v.vals, B, C, v.M, v.K, accumulate)
+    if (st) {
+      if (N == 4) SC_ROW(kRowStagedRows, 4, true);
+      else if (N == 2) SC_ROW(kRowStagedRows, 2, true);
+      else SC_ROW(kRowStagedRows, 1, true);
+    } else {
+      if (N == 4) SC_ROW(kRowSpmvRows, 4, false);
+      else if (N == 2) SC_ROW(kRowSpmvRows, 2, false);
+      else SC_ROW(kRowSpmvRows, 1, false);
+    }
 #undef SC_ROW
     return hipGetLastError();
   }

@@ -1021,8 +1021,10 @@ int sc_plan_describe(const sc_plan *p, int32_t N, char *buf, size_t buflen) {
       const sc::Geometry g = sc::geometry(p->km, N, w, p->K, p->view.max_pslots, p->view.max_pvals, p->view.a_bytes,
                                    p->nslots / std::max(1, p->npanels), p->npanels);
       if (sc::use_row_spmv(p->view, p->km, N, w)) {
-        d = "row_spmv_kernel km=1 V=" + std::to_string(N) + " rows_per_workgroup=" + std::to_string(sc::kRowSpmvRows) + " grid=" +
-            std::to_string((p->M + sc::kRowSpmvRows - 1) / sc::kRowSpmvRows);
+        const bool st = sc::row_spmv_staged(p->view, N);
+        const int rows = st ? sc::kRowStagedRows : sc::kRowSpmvRows;
+        d = "row_spmv_kernel km=1 V=" + std::to_string(N) + " rows_per_workgroup=" + std::to_string(rows) +
+            (st ? " B_in_lds=1" : "") + " grid=" + std::to_string((p->M + rows - 1) / rows);
       } else if (!g.wide && sc::gather_lds_f32(N, w, p->km, p->view.max_pslots, p->view.max_pvals)) {
         d = "gather_kernel km=" + std::to_string(p->km) + " V=" + std::to_string(N) + " waves=" +
             std::to_string(w) + " grid=" + std::to_string(p->npanels);

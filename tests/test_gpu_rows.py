@@ -237,3 +237,48 @@ def test_row_spmv_kernel_tails_empty_rows_padding(kn, drop, accumulate, n):
             assert np.all(C[lens == 0] == 0)
         else:
             assert np.array_equal(C[lens == 0], C0[lens == 0])
+
+
+@pytest.mark.parametrize("n", [1, 2, 4])
+def test_row_kernel_b_in_lds(n):
+    # 4100 rows (a partial workgroup of 16 rows at the end, empty rows) over
+    # K = 2048 at 5 % density: about 100 entries per B row, so the row kernel
+    # copies B into LDS first; plain and accumulating
+    rng = np.random.default_rng(21 + n)
+    A, B = synth_case(4100, 2048, 0.05, n, seed=0x5EED0000 + 9700 + n)
+    ip, ix, dx = A.arrays()
+    keep = np.ones(A.nnz, bool)
+    for r in (0, 17, 4099):
+        keep[ip[r]:ip[r + 1]] = False  # rows 0, 17 and the last one empty
+    rows = np.repeat(np.arange(4100), np.diff(ip))
+    dense_rows, dense_cols, dense_vals = rows[keep], ix[keep], dx[keep]
+    order = np.lexsort((dense_cols, dense_rows))
+    ptr = np.zeros(4101, np.int32)
+    np.add.at(ptr, dense_rows[order] + 1, 1)
+    A = sc_amd.Csr.from_arrays(4100, 2048, np.cumsum(ptr).astype(np.int32), dense_cols[order], dense_vals[order])
+    plan, C = run(A, B, 4, 1, 0)
+    assert "B_in_lds=1" in plan.describe(n), plan.describe(n)
+    err, _ = oracle_check(A, B, C)
+    assert err <= REL_TOL, (n, err)
+    assert np.all(C[[0, 17, 4099]] == 0)
+    C0 = rng.uniform(-1, 1, size=(4100, n)).astype(np.float32)
+    _, Ca = run(A, B, 4, 1, 0, accumulate=C0)
+    assert oracle_check_acc(A, B, Ca, C0) <= REL_TOL
+
+
+def test_row_kernel_b_in_lds_spmv_exact():
+    # integer-valued A and x: the staged gathers give the exact sums
+    rng = np.random.default_rng(23)
+    m, k = 4096, 1024
+    mask = rng.random((m, k)) < 0.08
+    dense = np.where(mask, rng.integers(-3, 4, size=(m, k)), 0).astype(np.float64)
+    r, c = np.nonzero(dense)
+    ptr = np.zeros(m + 1, np.int32)
+    np.add.at(ptr, r + 1, 1)
+    A = sc_amd.Csr.from_arrays(m, k, np.cumsum(ptr).astype(np.int32), c.astype(np.int32), dense[r, c])
+    x = rng.integers(-4, 5, size=k).astype(np.float32)
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 1, 1), 0)
+    assert "B_in_lds=1" in plan.describe(1), plan.describe(1)
+    y = plan.spmv(torch.from_numpy(x).to(DEV))
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy(), (dense @ x.astype(np.float64)).astype(np.float32))
