@@ -97,7 +97,21 @@ struct DevView {
   long long a_bytes;      // bytes of the plan's column and value streams
   const int *row_len;     // km = 1 plans: slots of each panel (row) that its segment
                           // holds, without the 16-byte alignment padding; else null
+  const int *launch;      // [npanels * kLaunchInts] the panel kernel's workgroups in
+                          // launch order (PanelLaunch), one row per workgroup
 };
+
+// A row of DevView::launch: the panel workgroup x runs and its ranges, so a
+// workgroup finds all of them in one 32-byte scalar load.  Workgroups x,
+// x + C, x + 2C, ... (C the GPU's CU count) share a CU when the grid fits
+// the GPU at once (the dispatcher deals workgroups to the CUs in turn), so
+// the plan orders the panels to even out the slots each CU gathers (longest
+// panel first onto the least loaded CU).
+struct PanelLaunch {
+  int panel, slot0, slot1, seg0, seg1, val0, val1, pad;
+};
+constexpr int kLaunchInts = 8;
+static_assert(sizeof(PanelLaunch) == kLaunchInts * sizeof(int), "one 32-byte row per workgroup");
 
 // Chunk kernel: columns of B per chunk, B rows per K block (LDS tile), and
 // panels per row group (waves per workgroup).
@@ -439,28 +453,28 @@ __device__ __forceinline__ void stage_panel(int *lc, const int *__restrict__ col
 // cross-wave reduction.
 template <int KM, int V, bool STAGE, class D, class A>
 __global__ void __launch_bounds__(1024)
-    panel_kernel(const int4 *__restrict__ seg, const int *__restrict__ panel_seg,
-                 const int *__restrict__ panel_slot, const int *__restrict__ panel_val,
+    panel_kernel(const int4 *__restrict__ seg, const PanelLaunch *__restrict__ launch,
                  const int *__restrict__ cols, const float *__restrict__ vals,
                  const float *__restrict__ B, float *__restrict__ C, int M, int K, int N, int L,
                  int accumulate, int pack, int stage_cols) {
   extern __shared__ float red[];
-  const int panel = blockIdx.x;
+  const PanelLaunch pl = launch[blockIdx.x];
+  const int panel = pl.panel;
   const int W = blockDim.x >> 6;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int S = 64 / L;
   const int g = lane & (L - 1);
   const int s = lane / L;
-  const int p0 = panel_slot[panel];
-  const int p1 = panel_slot[panel + 1];
+  const int p0 = pl.slot0;
+  const int p1 = pl.slot1;
   // pack-aligned share of the panel's slots for this wave
   const int npk = (p1 - p0 + pack - 1) / pack;
   const int per = ((npk + W - 1) / W) * pack;
   const int a0 = p0 + w * per;
   const int a1 = min(p1, a0 + per);
-  const int sg0 = panel_seg[panel];
-  const int sg1 = panel_seg[panel + 1];
+  const int sg0 = pl.seg0;
+  const int sg1 = pl.seg1;
   const int row0 = panel * KM;
   const int LV = L * V;
   const int *cs = cols;
@@ -469,8 +483,8 @@ __global__ void __launch_bounds__(1024)
   // staged stream, so the reduction never overwrites the stream
   const int red_floats = W > 1 ? W * KM * LV : 0;  // as sized by geometry()
   auto stage = [&]() {
-    const int q0 = panel_val[panel];
-    const int q1 = panel_val[panel + 1];
+    const int q0 = pl.val0;
+    const int q1 = pl.val1;
     int *lc = reinterpret_cast<int *>(red + red_floats);
     float *lv = red + red_floats + stage_cols;
     stage_panel(lc, cols + p0, p1 - p0, lv, vals + q0, q1 - q0);
@@ -1060,32 +1074,32 @@ __device__ __forceinline__ void load_row(float (&b)[V], const WideArgs &a, int c
 // reused for the cross-wave reduction afterwards.
 template <int KM, int V, bool STAGE, class D>
 __global__ void __launch_bounds__(1024)
-    wide_kernel(const int4 *__restrict__ seg, const int *__restrict__ panel_seg,
-                const int *__restrict__ panel_slot, const int *__restrict__ panel_val,
+    wide_kernel(const int4 *__restrict__ seg, const PanelLaunch *__restrict__ launch,
                 const int *__restrict__ cols, const float *__restrict__ vals,
                 const float *__restrict__ B, float *__restrict__ C, int M, int K, int N,
                 int accumulate, int pack, int stage_cols) {
   extern __shared__ float smem[];
-  const int panel = blockIdx.x;
+  const PanelLaunch pl = launch[blockIdx.x];
+  const int panel = pl.panel;
   const int W = blockDim.x >> 6;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int p0 = panel_slot[panel];
-  const int p1 = panel_slot[panel + 1];
+  const int p0 = pl.slot0;
+  const int p1 = pl.slot1;
   const int npk = (p1 - p0 + pack - 1) / pack;
   const int per = ((npk + W - 1) / W) * pack;
   const int a0 = p0 + w * per;
   const int a1 = min(p1, a0 + per);
-  const int sg0 = panel_seg[panel];
-  const int sg1 = panel_seg[panel + 1];
+  const int sg0 = pl.seg0;
+  const int sg1 = pl.seg1;
   const int row0 = panel * KM;
   constexpr int CW = 64 * V;  // columns per chunk
 
   const int *cs = cols;
   const float *vs = vals;
   if constexpr (STAGE) {
-    const int q0 = panel_val[panel];
-    const int q1 = panel_val[panel + 1];
+    const int q0 = pl.val0;
+    const int q1 = pl.val1;
     int *lc = reinterpret_cast<int *>(smem);
     float *lv = smem + stage_cols;
     stage_panel(lc, cols + p0, p1 - p0, lv, vals + q0, q1 - q0);
@@ -1153,8 +1167,8 @@ __global__ void __launch_bounds__(1024)
     }
     if constexpr (STAGE) {
       if (cbase + CW < N) {  // restage: the reduction overwrote the stream
-        const int q0 = panel_val[panel];
-        const int q1 = panel_val[panel + 1];
+        const int q0 = pl.val0;
+        const int q1 = pl.val1;
         int *lc = reinterpret_cast<int *>(smem);
         float *lv = smem + stage_cols;
         stage_panel(lc, cols + p0, p1 - p0, lv, vals + q0, q1 - q0);
@@ -1770,9 +1784,9 @@ hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int 
   dim3 grid((unsigned)v.npanels), block((unsigned)(64 * W));
   if (g.wide) {
 #define SC_WIDE(VV, ST)                                                                           \
-  hipLaunchKernelGGL((wide_kernel<KM, VV, ST, D>), grid, block, g.lds, stream, v.seg, v.panel_seg, \
-                     v.panel_slot, v.panel_val, v.cols, v.vals, B, C, v.M, v.K, N, accumulate,     \
-                     pack, g.stage_cols)
+  hipLaunchKernelGGL((wide_kernel<KM, VV, ST, D>), grid, block, g.lds, stream, v.seg,                  \
+                     reinterpret_cast<const PanelLaunch *>(v.launch), v.cols, v.vals, B, C, v.M, v.K, N,  \
+                     accumulate, pack, g.stage_cols)
     if (g.stage) {
       if (g.V == 4) SC_WIDE(4, true);
       else if (g.V == 2) SC_WIDE(2, true);
@@ -1798,9 +1812,9 @@ hipError_t launch_panels(const DevView &v, const float *B, float *C, int N, int 
   }
   const dim3 ngrid((unsigned)v.npanels, (unsigned)g.ny);
 #define SC_NARROW(VV, ST, AA)                                                                          \
-  hipLaunchKernelGGL((panel_kernel<KM, VV, ST, D, AA>), ngrid, block, g.lds, stream, v.seg, v.panel_seg,  \
-                     v.panel_slot, v.panel_val, v.cols, v.vals, B, C, v.M, v.K, N, g.L, accumulate, pack, \
-                     g.stage_cols)
+  hipLaunchKernelGGL((panel_kernel<KM, VV, ST, D, AA>), ngrid, block, g.lds, stream, v.seg,                \
+                     reinterpret_cast<const PanelLaunch *>(v.launch), v.cols, v.vals, B, C, v.M, v.K, N, g.L,  \
+                     accumulate, pack, g.stage_cols)
   if (buffer_offsets_fit(v.K, N)) {
     if (g.stage) {
       if (g.V == 4) SC_NARROW(4, true, SegArgsBuf);
