@@ -1648,9 +1648,7 @@ __global__ void __launch_bounds__(64 * ROWS)
   // and the neighbouring rows' lines in the caches
   if constexpr (V == 1) {
     // scalar B values
-    for (int q = lane; q < nq; q += 64) {
-      const vec4i c = __builtin_nontemporal_load(c4 + q);
-      const vec4f v = __builtin_nontemporal_load(v4 + q);
+    auto quad = [&](const vec4i &c, const vec4f &v, int q) __attribute__((always_inline)) {
       const int e = q * 4;
       const float x0 = b_row(c.x)[0];  // e < n for every q < nq
       const float x1 = e + 1 < n ? b_row(c.y)[0] : 0.f;
@@ -1660,6 +1658,24 @@ __global__ void __launch_bounds__(64 * ROWS)
       if (e + 1 < n) acc[0] = __builtin_fmaf(v.y, x1, acc[0]);
       if (e + 2 < n) acc[0] = __builtin_fmaf(v.z, x2, acc[0]);
       if (e + 3 < n) acc[0] = __builtin_fmaf(v.w, x3, acc[0]);
+    };
+    if constexpr (STAGE) {
+      // two of the lane's quads in flight together (the second clamped into the row)
+      for (int q = lane; q < nq; q += 128) {
+        const int q2 = min(q + 64, nq - 1);
+        const vec4i c = __builtin_nontemporal_load(c4 + q);
+        const vec4f v = __builtin_nontemporal_load(v4 + q);
+        const vec4i c2 = __builtin_nontemporal_load(c4 + q2);
+        const vec4f v2 = __builtin_nontemporal_load(v4 + q2);
+        quad(c, v, q);
+        if (q + 64 < nq) quad(c2, v2, q + 64);
+      }
+    } else {
+      for (int q = lane; q < nq; q += 64) {
+        const vec4i c = __builtin_nontemporal_load(c4 + q);
+        const vec4f v = __builtin_nontemporal_load(v4 + q);
+        quad(c, v, q);
+      }
     }
   } else
   for (int q = lane; q < nq; q += 64) {
