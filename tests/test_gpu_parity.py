@@ -387,3 +387,31 @@ def test_tiled_first_launch_captured_in_a_graph():
         assert oracle_check(A, B, C)[0] <= REL_TOL, i
         ref = C if ref is None else ref
         assert np.array_equal(C, ref), i
+
+
+@pytest.mark.parametrize("n", [32, 40, 128])
+def test_launch_order_with_skewed_panels(n):
+    # 1031 panels (four groups of CUs hold one more panel than the rest) whose
+    # slot counts differ by 30x: the plan's launch order moves most panels
+    # to another workgroup, and every panel must still be run exactly once
+    rng = np.random.default_rng(0x5EED0000 + 9100 + n)
+    m, k = 4 * 1031 - 2, 640
+    dens = np.where(np.arange(m) % 97 < 9, 0.6, 0.02)
+    mask = rng.random((m, k)) < dens[:, None]
+    vals = rng.standard_normal(int(mask.sum())) * 0.05
+    ip = np.concatenate([[0], np.cumsum(mask.sum(1))]).astype(np.int32)
+    ix = np.nonzero(mask)[1].astype(np.int32)
+    A = sc_amd.Csr.from_arrays(m, k, ip, ix, vals.astype(np.float32).astype(np.float64))
+    B = sc_amd.synth_dense(k * n, 0x5EED0000 + 9200 + n).reshape(k, n)
+    for km in (4, 3):
+        C = run_spmm(A, B, km, 1)
+        err, _ = oracle_check(A, B, C)
+        assert err <= REL_TOL, (km, err)
+    # the one-row layout of the same slots (4122 one-row panels)
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1), sc_amd.PLAN_ROWS)
+    Bt = torch.from_numpy(np.ascontiguousarray(B, np.float32)).to(DEV)
+    Ct = torch.full((m, n), float("nan"), device=DEV)
+    plan.spmm(Bt, Ct)
+    torch.cuda.synchronize()
+    err, _ = oracle_check(A, B, Ct.cpu().numpy())
+    assert err <= REL_TOL, ("rows", plan.describe(n), err)
