@@ -136,7 +136,12 @@ void sc_cfmtx_free(sc_cfmtx *cf);
  * the one-row layout while its B-row gathers (4 * stored entries * N bytes)
  * total under 128 MiB, the km-row pattern layout above; sc_spmm_f16 follows
  * the same rule when the rows fit its LDS staging.  sc_spmm_generated always
- * runs the pattern layout. */
+ * runs the pattern layout.
+ * Concurrency: a plan holds no launch state unless it was built with
+ * SC_PLAN_TILED or SC_PLAN_BANDS, so its launches may run at once on distinct
+ * streams.  The split-K kernels of those two flags keep partial sums and
+ * arrival counters in the plan's workspace: launches of such a plan must be
+ * ordered (one stream, or events between streams). */
 
 /* allocateAndCopyMixedFormat (example_cuda/spmm_demo_gpu_utils.h:207-245) and
  * the constructors of the generated classes SpMMMixePatternGeneralCacheLess /
