@@ -415,3 +415,22 @@ def test_launch_order_with_skewed_panels(n):
     torch.cuda.synchronize()
     err, _ = oracle_check(A, B, Ct.cpu().numpy())
     assert err <= REL_TOL, ("rows", plan.describe(n), err)
+
+
+def test_default_plan_launches_on_two_streams_at_once():
+    # a default plan holds no launch state: launches of one plan on two
+    # streams, interleaved with no ordering between them, both match the oracle
+    A, B1 = synth_case(1024, 768, 0.1, 128, seed=0x5EED0000 + 9300)
+    B2 = sc_amd.synth_dense(768 * 128, 0x5EED0000 + 9301).reshape(768, 128)
+    plan = sc_amd.Plan(sc_amd.Cfmtx.build(A, 4, 1), 0)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    Bt = [torch.from_numpy(B1).to(DEV), torch.from_numpy(B2).to(DEV)]
+    Ct = [torch.full((1024, 128), float("nan"), device=DEV) for _ in range(2)]
+    torch.cuda.synchronize()
+    for _ in range(8):
+        plan.spmm(Bt[0], Ct[0], stream=s1)
+        plan.spmm(Bt[1], Ct[1], stream=s2)
+    torch.cuda.synchronize()
+    for B, Cg in ((B1, Ct[0]), (B2, Ct[1])):
+        err, _ = oracle_check(A, B, Cg.cpu().numpy())
+        assert err <= REL_TOL, err
