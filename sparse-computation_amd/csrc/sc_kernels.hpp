@@ -97,11 +97,11 @@ struct DevView {
   long long a_bytes;      // bytes of the plan's column and value streams
   const int *row_len;     // km = 1 plans: slots of each panel (row) that its segment
                           // holds, without the 16-byte alignment padding; else null
-  const int *launch;      // [npanels * kLaunchInts] the panel kernel's workgroups in
-                          // launch order (PanelLaunch), one row per workgroup
+  const int *launch;      // [npanels * kLaunchInts] the panel and wide kernels' workgroups
+                          // in launch order (PanelLaunch), one row per workgroup
 };
 
-// A row of DevView::launch: the panel workgroup x runs and its ranges, so a
+// A row of DevView::launch: the panel that workgroup x runs and its ranges, so a
 // workgroup finds all of them in one 32-byte scalar load.  Workgroups x,
 // x + C, x + 2C, ... (C the GPU's CU count) share a CU when the grid fits
 // the GPU at once (the dispatcher deals workgroups to the CUs in turn), so
