@@ -434,3 +434,22 @@ def test_default_plan_launches_on_two_streams_at_once():
     for B, Cg in ((B1, Ct[0]), (B2, Ct[1])):
         err, _ = oracle_check(A, B, Cg.cpu().numpy())
         assert err <= REL_TOL, err
+
+
+@pytest.mark.parametrize("n", [32, 64, 128])
+def test_large_b_every_coarsen_factor(n):
+    # BASELINE config 2 as the sweep times it (same matrix seed and B): every
+    # km 1..6 x kn 1..8 file, on the default plan and on the pattern layout
+    A = sc_amd.Csr.synth_uniform(512, 512, 0.10, 0.05, 0x5EED0000 + 2000)
+    B = sc_amd.synth_dense(512 * n, 0x5EED0000 + 500 + n).reshape(512, n)
+    Bt = torch.from_numpy(B).to(DEV)
+    for km in range(1, 7):
+        for kn in range(1, 9):
+            cf = sc_amd.Cfmtx.build(A, km, kn)
+            for flags in (0, PAT):
+                plan = sc_amd.Plan(cf, flags)
+                Ct = torch.full((512, n), float("nan"), device=DEV)
+                plan.spmm(Bt, Ct)
+                torch.cuda.synchronize()
+                err, _ = oracle_check(A, B, Ct.cpu().numpy())
+                assert err <= REL_TOL, (km, kn, flags, plan.describe(n), err)
